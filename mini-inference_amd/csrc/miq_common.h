@@ -1,0 +1,133 @@
+// Shared device/host helpers for libmiq (gfx950 only).
+//
+// Numeric conventions follow what PyTorch does on the CPU for the same formulas:
+//   * bf16 values are stored as raw uint16 and widened by a 16-bit shift (exact);
+//   * float -> bf16 is round-to-nearest-even (torch's c10::BFloat16 constructor);
+//   * float -> e4m3fn is round-to-nearest-even with subnormals (torch's
+//     Float8_e4m3fn constructor) for inputs already clamped to +-448.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/miq.h"
+
+namespace miq {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+__host__ __device__ inline float bf16_to_f32(uint16_t h) {
+  union { uint32_t u; float f; } v;
+  v.u = static_cast<uint32_t>(h) << 16;
+  return v.f;
+}
+
+__host__ __device__ inline uint16_t f32_to_bf16(float f) {
+  union { uint32_t u; float f; } v;
+  v.f = f;
+  uint32_t u = v.u;
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return 0x7fc0;  // NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__host__ __device__ inline float f16_to_f32(uint16_t h) {
+  return static_cast<float>(*reinterpret_cast<const _Float16*>(&h));
+}
+
+__host__ __device__ inline uint16_t f32_to_f16(float f) {
+  _Float16 h = static_cast<_Float16>(f);
+  return *reinterpret_cast<uint16_t*>(&h);
+}
+
+// e4m3fn decode: 1 sign, 4 exponent (bias 7), 3 mantissa bits; 0x7f/0xff are NaN.
+__host__ __device__ inline float fp8_to_f32(uint8_t b) {
+  const uint32_t s = b & 0x80u, e = (b >> 3) & 0xfu, m = b & 0x7u;
+  float mag;
+  if (e == 0) {
+    mag = static_cast<float>(m) * 0.001953125f;  // m * 2^-9
+  } else if (e == 15 && m == 7) {
+    mag = __builtin_nanf("");
+  } else {
+    union { uint32_t u; float f; } v;
+    v.u = ((e + 120u) << 23) | (m << 20);  // (1 + m/8) * 2^(e-7)
+    mag = v.f;
+  }
+  return s ? -mag : mag;
+}
+
+// e4m3fn encode, round-to-nearest-even, for |x| <= 448 (callers clamp first, as the
+// reference formulas do). Subnormals (|x| < 2^-6) are multiples of 2^-9.
+__host__ __device__ inline uint8_t f32_to_fp8(float x) {
+  union { uint32_t u; float f; } v;
+  v.f = x;
+  const uint32_t sign = (v.u >> 24) & 0x80u;
+  const uint32_t a = v.u & 0x7fffffffu;
+  if (a > 0x7f800000u) return static_cast<uint8_t>(sign | 0x7f);  // NaN
+  if (a < 0x3c800000u) {  // below 2^-6: subnormal grid of 2^-9
+    v.u = a;
+    const float q = __builtin_rintf(v.f * 512.0f);  // exact scaling, RNE
+    return static_cast<uint8_t>(sign | static_cast<uint32_t>(q));  // q == 8 encodes 2^-6
+  }
+  // normal: keep 3 mantissa bits with RNE on the 20 dropped bits
+  const uint32_t r = a + 0x7ffffu + ((a >> 20) & 1u);
+  const uint32_t e = (r >> 23) - 120u;  // rebias 127 -> 7
+  const uint32_t m = (r >> 20) & 7u;
+  uint32_t code = (e << 3) | m;
+  if (code > 0x7eu) code = 0x7eu;  // saturate at 448 (inputs are clamped, kept for safety)
+  return static_cast<uint8_t>(sign | code);
+}
+
+__device__ inline float load_scalar(const void* p, int dtype, int64_t i) {
+  switch (dtype) {
+    case MIQ_BF16: return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+    case MIQ_F16: return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+    default: return static_cast<const float*>(p)[i];
+  }
+}
+
+// Round a float to the storage precision of `dtype` and back.
+__device__ inline float round_to(float f, int dtype) {
+  switch (dtype) {
+    case MIQ_BF16: return bf16_to_f32(f32_to_bf16(f));
+    case MIQ_F16: return f16_to_f32(f32_to_f16(f));
+    default: return f;
+  }
+}
+
+__device__ inline void store_scalar(void* p, int dtype, int64_t i, float f) {
+  switch (dtype) {
+    case MIQ_BF16: static_cast<uint16_t*>(p)[i] = f32_to_bf16(f); break;
+    case MIQ_F16: static_cast<uint16_t*>(p)[i] = f32_to_f16(f); break;
+    default: static_cast<float*>(p)[i] = f; break;
+  }
+}
+
+__device__ inline float wave_max(float v) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ inline float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace miq
+
+// ----------------------------------------------------------------- host-side error plumbing
+namespace miq {
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace miq
+
+#define MIQ_REQUIRE(cond, ...)                 \
+  do {                                         \
+    if (!(cond)) {                             \
+      ::miq::set_error(__VA_ARGS__);           \
+      return MIQ_ERR_INVALID;                  \
+    }                                          \
+  } while (0)

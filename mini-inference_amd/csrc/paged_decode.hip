@@ -1,0 +1,424 @@
+// Split-KV paged decode attention over bf16 / fp8 (e4m3fn) / int8 KV caches, gfx950.
+//
+// Work decomposition: one workgroup per (partition of `partition` tokens, kv head,
+// request). All GROUP = H / KV query heads of the kv head are handled together, so every
+// K/V byte is read from HBM once (not once per query head). The four wavefronts of a
+// workgroup take consecutive quarters of the partition and walk it 32 tokens at a time:
+//
+//   scores  S[h, t] = q[h] . K[t]      v_mfma_f32_16x16x32_bf16, A = q (rows = heads,
+//                                       zero-padded to 16), B = K^T (columns = tokens);
+//                                       each lane loads 32 contiguous bytes of its
+//                                       token's K row and dequantizes in registers
+//   online softmax over t              fp32, exp2 domain; row max by lane shuffles
+//   O[h, d] += P[h, t] V[t, d]         same MFMA, A = P (bf16, staged in LDS), B = V
+//                                       (dequantized to bf16 and written transposed,
+//                                       V^T[d][t], into the wavefront's LDS slice)
+//
+// 8-bit scales are applied outside the MFMAs: k_scale multiplies the score of its token,
+// v_scale multiplies P before it is rounded to bf16, so the MFMA operands are exact
+// decodes of the stored codes. The wavefronts' softmax states are merged through LDS;
+// each workgroup writes its normalised partial output and log-sum-exp, and a second
+// kernel merges the partitions of each (request, head).
+#include "miq_common.h"
+
+namespace miq {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kWaves = 4;
+constexpr int kStep = 32;            // tokens per wavefront iteration
+constexpr int kPRow = kStep + 8;     // P[h][t] row stride (bf16)
+constexpr int kVRow = kStep + 8;     // V^T[d][t] row stride (bf16)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct AttnParams {
+  const uint16_t* q;
+  int64_t qs_b, qs_h;
+  const uint8_t* k;
+  const uint8_t* v;
+  int kv_dtype;
+  int64_t kvs_t, kvs_h;  // in elements
+  const void* ks;
+  const void* vs;
+  int s_dtype;
+  int64_t ss_t, ss_h;
+  const int32_t* bt;
+  int64_t bt_stride;
+  const int32_t* lens;
+  int H, KV, group, page;
+  float sm_scale;
+  int partition, max_parts;
+  float* o_part;
+  float* lse_part;
+};
+
+__device__ inline bf16x8 bf16x8_from(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  i32x4 v = {(int)a, (int)b, (int)c, (int)d};
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// 4 fp8 codes -> 2 dwords of bf16 pairs (exact)
+__device__ inline void fp8x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false));
+  hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true));
+}
+
+// 4 int8 codes -> 2 dwords of bf16 pairs (exact: |q| <= 128)
+__device__ inline void i8x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  const float f0 = (float)(int8_t)(w & 0xff), f1 = (float)(int8_t)((w >> 8) & 0xff);
+  const float f2 = (float)(int8_t)((w >> 16) & 0xff), f3 = (float)(int8_t)(w >> 24);
+  lo = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0), 0x07060302u);
+  hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f3), __builtin_bit_cast(uint32_t, f2), 0x07060302u);
+}
+
+template <int KVT>
+__device__ inline void bytes8_to_bf16(uint32_t w0, uint32_t w1, uint32_t out[4]) {
+  if (KVT == MIQ_FP8_E4M3) {
+    fp8x4_to_bf16(w0, out[0], out[1]);
+    fp8x4_to_bf16(w1, out[2], out[3]);
+  } else {
+    i8x4_to_bf16(w0, out[0], out[1]);
+    i8x4_to_bf16(w1, out[2], out[3]);
+  }
+}
+
+__device__ inline f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ inline void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// max / sum over the 16 lanes that share lane / 16
+__device__ inline float max16(float v) {
+  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ inline float sum16(float v) {
+  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+template <int KVT, bool HAS_SCALE>
+__global__ void __launch_bounds__(kWaves * 64)
+paged_decode_split_kernel(AttnParams p) {
+  const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int L = p.lens[b];
+  const int p0 = part * p.partition;
+  if (part > 0 && p0 >= L) return;  // partition beyond this request's context
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int GROUP = p.group;
+
+  __shared__ __align__(16) uint16_t s_p[kWaves][16 * kPRow];
+  // per wavefront: V^T[d][t] during the token loop, then its O rows for the merge
+  __shared__ __align__(16) uint16_t s_vt[kWaves][kD * kVRow];
+  __shared__ float s_m[kWaves][16], s_l[kWaves][16];
+  static_assert(16 * (kD + 4) * sizeof(float) <= kD * kVRow * sizeof(uint16_t), "O rows must fit");
+
+  // q fragments: lane row r = head within the group, 32 d at g * 32
+  bf16x8 qf[4];
+  {
+    const bool real = r < GROUP;
+    const uint16_t* qp = p.q + (int64_t)b * p.qs_b + (int64_t)(kvh * GROUP + (real ? r : 0)) * p.qs_h + g * 32;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint4 u = real ? *reinterpret_cast<const uint4*>(qp + j * 8) : make_uint4(0, 0, 0, 0);
+      qf[j] = bf16x8_from(u.x, u.y, u.z, u.w);
+    }
+  }
+  // rows of P for heads >= GROUP stay zero
+  for (int i = lane; i < 16 * kPRow; i += 64) s_p[wv][i] = 0;
+
+  const int per_wave = p.partition / kWaves;
+  const int t_begin = p0 + wv * per_wave;
+  const int t_end = min(t_begin + per_wave, L);
+  const float qk_scale = p.sm_scale * kLog2e;
+
+  float m_run[4], l_run[4];
+  f32x4 o_acc[8];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) { m_run[v] = -__builtin_inff(); l_run[v] = 0.f; }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o_acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  constexpr int ESZ = KVT == MIQ_BF16 ? 2 : 1;
+  const int64_t head_off = (int64_t)kvh * p.kvs_h * ESZ;
+  uint16_t* vt = s_vt[wv];
+  uint16_t* pp = s_p[wv];
+
+  for (int t0 = t_begin; t0 < t_end; t0 += kStep) {
+    // ---- K: lane handles token t0 + 16 * c + r, 32 d at g * 32
+    float sc[2][4];
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int t = t0 + c * 16 + r;
+      const bool valid = t < t_end;
+      const int tc = valid ? t : t_end - 1;
+      const int64_t slot = (int64_t)p.bt[(int64_t)b * p.bt_stride + tc / p.page] * p.page + tc % p.page;
+      const uint8_t* kp = p.k + slot * p.kvs_t * ESZ + head_off + g * 32 * ESZ;
+      bf16x8 kf[4];
+      if (KVT == MIQ_BF16) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint4 u = *reinterpret_cast<const uint4*>(kp + j * 16);
+          kf[j] = bf16x8_from(u.x, u.y, u.z, u.w);
+        }
+      } else {
+        const uint4 u0 = *reinterpret_cast<const uint4*>(kp);
+        const uint4 u1 = *reinterpret_cast<const uint4*>(kp + 16);
+        uint32_t o[4];
+        bytes8_to_bf16<KVT>(u0.x, u0.y, o); kf[0] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        bytes8_to_bf16<KVT>(u0.z, u0.w, o); kf[1] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        bytes8_to_bf16<KVT>(u1.x, u1.y, o); kf[2] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        bytes8_to_bf16<KVT>(u1.z, u1.w, o); kf[3] = bf16x8_from(o[0], o[1], o[2], o[3]);
+      }
+      f32x4 s4 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s4 = mfma16(qf[j], kf[j], s4);
+      // C layout: lane holds heads 4 * g + v of token column r
+      float kscale = qk_scale;
+      if (HAS_SCALE) kscale *= load_scalar(p.ks, p.s_dtype, slot * p.ss_t + (int64_t)kvh * p.ss_h);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) sc[c][v] = valid ? s4[v] * kscale : -__builtin_inff();
+    }
+    // ---- online softmax (per head = per (g, v)); 16 lanes of a row group share a head
+    float alpha[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float mt = max16(fmaxf(sc[0][v], sc[1][v]));
+      const float mn = fmaxf(m_run[v], mt);
+      // a head row that has seen no valid token keeps m = -inf; guard the exp2 arguments
+      const float msafe = mn == -__builtin_inff() ? 0.f : mn;
+      alpha[v] = exp2f(m_run[v] - msafe);
+      m_run[v] = mn;
+      const float e0 = exp2f(sc[0][v] - msafe), e1 = exp2f(sc[1][v] - msafe);
+      sc[0][v] = e0;
+      sc[1][v] = e1;
+      l_run[v] = l_run[v] * alpha[v] + e0 + e1;
+    }
+    // ---- P (scaled by v_scale) -> LDS rows = heads
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const int t = t0 + c * 16 + r;
+      float vsc = 1.f;
+      if (HAS_SCALE) {
+        const int tc = t < t_end ? t : t_end - 1;
+        const int64_t slot = (int64_t)p.bt[(int64_t)b * p.bt_stride + tc / p.page] * p.page + tc % p.page;
+        vsc = load_scalar(p.vs, p.s_dtype, slot * p.ss_t + (int64_t)kvh * p.ss_h);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int h = g * 4 + v;
+        if (h < GROUP) pp[h * kPRow + c * 16 + r] = f32_to_bf16(sc[c][v] * vsc);
+      }
+    }
+    // ---- V: lane loads tokens t0 + 4 * (lane / 8) + i (i < 4), 16 d at 16 * (lane % 8)
+    {
+      const int tq = (lane >> 3) * 4, dseg = (lane & 7) * 16;
+      uint32_t vals[4][8];  // [token][bf16 pair]
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + tq + i;
+        const int tc = t < t_end ? t : t_end - 1;
+        const int64_t slot = (int64_t)p.bt[(int64_t)b * p.bt_stride + tc / p.page] * p.page + tc % p.page;
+        const uint8_t* vp = p.v + slot * p.kvs_t * ESZ + head_off + dseg * ESZ;
+        if (KVT == MIQ_BF16) {
+          const uint4 u0 = *reinterpret_cast<const uint4*>(vp);
+          const uint4 u1 = *reinterpret_cast<const uint4*>(vp + 16);
+          vals[i][0] = u0.x; vals[i][1] = u0.y; vals[i][2] = u0.z; vals[i][3] = u0.w;
+          vals[i][4] = u1.x; vals[i][5] = u1.y; vals[i][6] = u1.z; vals[i][7] = u1.w;
+        } else {
+          const uint4 u = *reinterpret_cast<const uint4*>(vp);
+          uint32_t o[4];
+          bytes8_to_bf16<KVT>(u.x, u.y, o);
+          vals[i][0] = o[0]; vals[i][1] = o[1]; vals[i][2] = o[2]; vals[i][3] = o[3];
+          bytes8_to_bf16<KVT>(u.z, u.w, o);
+          vals[i][4] = o[0]; vals[i][5] = o[1]; vals[i][6] = o[2]; vals[i][7] = o[3];
+        }
+        if (t >= t_end) {  // zero V of masked tokens (P is 0 there, but 0 * NaN is NaN)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vals[i][e] = 0;
+        }
+      }
+      // transpose: for each d, the 4 tokens' values -> one 8-byte LDS write
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+#pragma unroll
+        for (int hfl = 0; hfl < 2; ++hfl) {
+          const uint32_t sel = hfl ? 0x07060302u : 0x05040100u;
+          const uint32_t a01 = __builtin_amdgcn_perm(vals[1][e], vals[0][e], sel);
+          const uint32_t a23 = __builtin_amdgcn_perm(vals[3][e], vals[2][e], sel);
+          const int d = dseg + e * 2 + hfl;
+          *reinterpret_cast<uint2*>(vt + d * kVRow + tq) = make_uint2(a01, a23);
+        }
+      }
+    }
+    wave_lds_sync();
+    // ---- O[h, d] = alpha * O + P V
+    {
+      const uint4 pa = *reinterpret_cast<const uint4*>(pp + r * kPRow + g * 8);
+      const bf16x8 pf = bf16x8_from(pa.x, pa.y, pa.z, pa.w);
+      // alpha of the heads this lane's accumulator rows belong to: rows 4 * g + v
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) o_acc[j][v] *= alpha[v];
+        const uint4 vb = *reinterpret_cast<const uint4*>(vt + (j * 16 + r) * kVRow + g * 8);
+        o_acc[j] = mfma16(pf, bf16x8_from(vb.x, vb.y, vb.z, vb.w), o_acc[j]);
+      }
+    }
+    wave_lds_sync();
+  }
+
+  // ---- merge the four wavefronts: heads 4 * g + v, d = 16 * j + r
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const float lsum = sum16(l_run[v]);
+    if (r == 0) {
+      s_m[wv][g * 4 + v] = m_run[v];
+      s_l[wv][g * 4 + v] = lsum;
+    }
+  }
+  float* s_o_w = reinterpret_cast<float*>(s_vt[wv]);  // this wavefront's loop is done with it
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) s_o_w[(g * 4 + v) * (kD + 4) + j * 16 + r] = o_acc[j][v];
+  __syncthreads();
+
+  // 256 threads: thread -> (head hh = tid / 16 if < GROUP, 8 d values)
+  const int hh = tid >> 4, dq = (tid & 15) * 8;
+  if (hh < GROUP) {
+    float mx = -__builtin_inff();
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][hh]);
+    const float ms = mx == -__builtin_inff() ? 0.f : mx;
+    float lt = 0.f, sw[kWaves];
+    for (int w = 0; w < kWaves; ++w) {
+      sw[w] = exp2f(s_m[w][hh] - ms);
+      lt += s_l[w][hh] * sw[w];
+    }
+    const int h = kvh * GROUP + hh;
+    const int64_t base = ((int64_t)b * p.H + h) * p.max_parts + part;
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    float* op = p.o_part + base * kD + dq;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float o = 0.f;
+      for (int w = 0; w < kWaves; ++w)
+        o += reinterpret_cast<const float*>(s_vt[w])[hh * (kD + 4) + dq + e] * sw[w];
+      op[e] = o * inv;
+    }
+    if ((tid & 15) == 0) p.lse_part[base] = lt > 0.f ? (mx + log2f(lt)) * kLn2 : -__builtin_inff();
+  }
+}
+
+// out[b, h] = sum_s exp(lse_s - max) o_s / sum_s exp(lse_s - max)
+__global__ void __launch_bounds__(kD)
+paged_decode_merge_kernel(const float* __restrict__ o_part, const float* __restrict__ lse_part,
+                          const int32_t* __restrict__ lens, int H, int partition, int max_parts,
+                          uint16_t* __restrict__ out, int64_t os_b, int64_t os_h) {
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int L = lens[b];
+  int np = (L + partition - 1) / partition;
+  if (np < 1) np = 1;
+  if (np > max_parts) np = max_parts;  // a context longer than the caller's max_len is cut
+  const int64_t base = ((int64_t)b * H + h) * max_parts;
+  float mx = -__builtin_inff();
+  for (int s = 0; s < np; ++s) mx = fmaxf(mx, lse_part[base + s]);
+  float num = 0.f, den = 0.f;
+  if (mx != -__builtin_inff()) {
+    for (int s = 0; s < np; ++s) {
+      const float w = __expf(lse_part[base + s] - mx);
+      num += w * o_part[(base + s) * kD + d];
+      den += w;
+    }
+  }
+  out[(int64_t)b * os_b + (int64_t)h * os_h + d] = f32_to_bf16(den > 0.f ? num / den : 0.f);
+}
+
+template <int KVT, bool HS>
+void launch_split(const AttnParams& p, dim3 grid, hipStream_t st) {
+  hipLaunchKernelGGL((paged_decode_split_kernel<KVT, HS>), grid, dim3(kWaves * 64), 0, st, p);
+}
+
+}  // namespace
+}  // namespace miq
+
+using namespace miq;
+
+extern "C" int miq_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                const void* k_cache, const void* v_cache, int kv_dtype,
+                                int64_t kv_stride_t, int64_t kv_stride_h,
+                                const void* k_scale, const void* v_scale, int scale_dtype,
+                                int64_t s_stride_t, int64_t s_stride_h,
+                                const int32_t* block_table, int64_t bt_stride, const int32_t* seq_lens,
+                                int64_t B, int64_t H, int64_t KV, int64_t D, int64_t page,
+                                float sm_scale, int64_t partition, int64_t max_parts,
+                                float* o_part, float* lse_part,
+                                void* out, int64_t out_stride_b, int64_t out_stride_h, void* stream) {
+  MIQ_REQUIRE(D == kD, "paged_decode: head_dim %lld unsupported (128 only)", (long long)D);
+  MIQ_REQUIRE(KV >= 1 && H % KV == 0 && H / KV <= 16, "paged_decode: H=%lld KV=%lld (group <= 16)",
+              (long long)H, (long long)KV);
+  MIQ_REQUIRE(kv_dtype == MIQ_BF16 || kv_dtype == MIQ_FP8_E4M3 || kv_dtype == MIQ_INT8,
+              "paged_decode: kv dtype must be bf16, fp8 or int8");
+  MIQ_REQUIRE(partition >= 128 && partition % 128 == 0, "paged_decode: partition must be a multiple of 128");
+  MIQ_REQUIRE(page >= 1 && B >= 1 && max_parts >= 1 && B < 65536 && KV < 65536 && max_parts < (1 << 30),
+              "paged_decode: bad sizes");
+  MIQ_REQUIRE((k_scale == nullptr) == (v_scale == nullptr), "paged_decode: give both scales or neither");
+  MIQ_REQUIRE(kv_dtype != MIQ_BF16 || k_scale == nullptr, "paged_decode: bf16 cache takes no scales");
+  MIQ_REQUIRE(scale_dtype == MIQ_F32 || scale_dtype == MIQ_BF16 || scale_dtype == MIQ_F16,
+              "paged_decode: bad scale dtype");
+  const int esz = kv_dtype == MIQ_BF16 ? 2 : 1;
+  MIQ_REQUIRE((kv_stride_t * esz) % 16 == 0 && (kv_stride_h * esz) % 16 == 0 &&
+                  ((reinterpret_cast<uintptr_t>(k_cache) | reinterpret_cast<uintptr_t>(v_cache)) & 15) == 0,
+              "paged_decode: K/V rows must be 16-byte aligned");
+  MIQ_REQUIRE(q_stride_h % 8 == 0 && q_stride_b % 8 == 0 && (reinterpret_cast<uintptr_t>(q) & 15) == 0,
+              "paged_decode: q rows must be 16-byte aligned");
+  AttnParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.qs_b = q_stride_b;
+  p.qs_h = q_stride_h;
+  p.k = static_cast<const uint8_t*>(k_cache);
+  p.v = static_cast<const uint8_t*>(v_cache);
+  p.kv_dtype = kv_dtype;
+  p.kvs_t = kv_stride_t;
+  p.kvs_h = kv_stride_h;
+  p.ks = k_scale;
+  p.vs = v_scale;
+  p.s_dtype = scale_dtype;
+  p.ss_t = s_stride_t;
+  p.ss_h = s_stride_h;
+  p.bt = block_table;
+  p.bt_stride = bt_stride;
+  p.lens = seq_lens;
+  p.H = (int)H;
+  p.KV = (int)KV;
+  p.group = (int)(H / KV);
+  p.page = (int)page;
+  p.sm_scale = sm_scale;
+  p.partition = (int)partition;
+  p.max_parts = (int)max_parts;
+  p.o_part = o_part;
+  p.lse_part = lse_part;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)max_parts, (unsigned)KV, (unsigned)B);
+  const bool hs = k_scale != nullptr;
+  if (kv_dtype == MIQ_BF16) launch_split<MIQ_BF16, false>(p, grid, st);
+  else if (kv_dtype == MIQ_FP8_E4M3) {
+    if (hs) launch_split<MIQ_FP8_E4M3, true>(p, grid, st);
+    else launch_split<MIQ_FP8_E4M3, false>(p, grid, st);
+  } else {
+    if (hs) launch_split<MIQ_INT8, true>(p, grid, st);
+    else launch_split<MIQ_INT8, false>(p, grid, st);
+  }
+  int rc = check_launch("paged_decode split");
+  if (rc) return rc;
+  hipLaunchKernelGGL(paged_decode_merge_kernel, dim3((unsigned)H, (unsigned)B), dim3(kD), 0, st, o_part,
+                     lse_part, seq_lens, (int)H, (int)partition, (int)max_parts,
+                     static_cast<uint16_t*>(out), out_stride_b, out_stride_h);
+  return check_launch("paged_decode merge");
+}

@@ -1,0 +1,60 @@
+"""Torch-facing wrappers of miq_moe_align and miq_w4a16_moe.
+
+moe_align keeps the contract of the reference (kernels/fused_moe/fused_moe_triton.py:8-39
+and csrc/moe_align.cu:5-88): (sorted_ids, expert_ids, num_padded) with the pairs of each
+expert padded to block_m by the sentinel T*k. fused_moe_int4 replaces the per-expert loop
+of QuantExperts.forward (engine/quantization/modules.py:55-75) for INT4 experts.
+"""
+import torch
+
+from kernels import _lib as L
+
+BLOCK_M = 16  # rows per expert tile of the grouped GEMMs
+
+
+def moe_align(topk_ids, num_experts, block_m):
+    L.require_device(topk_ids)
+    flat = topk_ids.reshape(-1)
+    if flat.dtype not in (torch.int32, torch.int64):
+        raise RuntimeError("moe_align: topk_ids must be int32 or int64")
+    flat = flat.contiguous()
+    num_pairs = flat.numel()
+    max_padded = num_pairs + num_experts * (block_m - 1)
+    max_blocks = (max_padded + block_m - 1) // block_m
+    dev = flat.device
+    sorted_ids = torch.empty(max_padded, dtype=torch.int32, device=dev)
+    expert_ids = torch.empty(max_blocks, dtype=torch.int32, device=dev)
+    num_padded = torch.empty(1, dtype=torch.int32, device=dev)
+    L.call("miq_moe_align", L.ptr(flat), L.dtype_code(flat.dtype), num_pairs, num_experts, block_m,
+           L.ptr(sorted_ids), L.ptr(expert_ids), L.ptr(num_padded), L.stream(dev))
+    return sorted_ids, expert_ids, num_padded
+
+
+def fused_moe_int4(hidden, topk_ids, topk_weights, gu_q, gu_scale, gu_zero, dn_q, dn_scale, dn_zero):
+    """out[t] = sum_j w[t, j] * down_e(silu(gate_e(x_t)) * up_e(x_t)), e = topk_ids[t, j].
+
+    hidden bf16 [T, H]; gu_q uint8 [E, 2I, H/2]; dn_q uint8 [E, H, I/2]; scale/zero
+    [E, rows, K/group] (zero may be None: symmetric codes)."""
+    L.require_device(hidden, topk_ids, topk_weights, gu_q, dn_q)
+    T, H = hidden.shape
+    E, two_i, _ = gu_q.shape
+    inter = two_i // 2
+    k = topk_ids.shape[-1]
+    group = H // gu_scale.shape[-1]
+    if dn_scale.shape[-1] * group != inter:
+        raise RuntimeError("fused_moe_int4: gate_up and down must share one group size")
+    sorted_ids, expert_ids, num_padded = moe_align(topk_ids, E, BLOCK_M)
+    h = hidden.contiguous()
+    w = topk_weights.to(torch.bfloat16).contiguous()
+    nbytes = L.load().miq_moe_workspace_bytes(T, k, E, H, inter)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=hidden.device)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=hidden.device)
+    sdt = gu_scale.dtype
+    L.call("miq_w4a16_moe", L.ptr(h), T, H, inter, E, k,
+           L.ptr(gu_q.contiguous()), L.ptr(gu_scale.contiguous()),
+           L.ptr(None if gu_zero is None else gu_zero.contiguous()),
+           L.ptr(dn_q.contiguous()), L.ptr(dn_scale.contiguous()),
+           L.ptr(None if dn_zero is None else dn_zero.contiguous()),
+           L.dtype_code(sdt), group, L.ptr(w), L.ptr(sorted_ids), L.ptr(expert_ids), L.ptr(num_padded),
+           L.ptr(ws), nbytes, L.ptr(out), L.stream(hidden.device))
+    return out

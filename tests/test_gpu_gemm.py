@@ -1,0 +1,164 @@
+"""Weight-only skinny GEMMs and the FP8 GEMM vs the fp32-accumulated CPU oracle.
+
+Tolerance: |got - want| <= 1e-2 + 2e-2 * |want| elementwise,
+want = the fp32-accumulated product on the dequantized weights evaluated in fp32
+(q * s + z exactly, as the kernels do). The reference's own bf16 formula
+(int4_wo.py:33-42 + base.py:20-24) rounds every dequantized weight to bf16 twice; at
+K = 9728 that alone moves outputs by up to ~0.04, so it is held to the norm-wise bound of
+the reference's test (tests/test_quantizaton.py:60-72, rel < 0.01), and the kernel output
+is checked against the reference formula to that same bound.
+"""
+import pytest
+import torch
+
+from oracle import quant as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+ATOL, RTOL = 1e-2, 2e-2
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def within(got, want, atol=ATOL, rtol=RTOL):
+    got = got.float().cpu()
+    want = want.float().cpu()
+    err = (got - want).abs()
+    bound = atol + rtol * want.abs()
+    worst = (err - bound).max().item()
+    assert worst <= 0, f"max excess {worst:.3e}, max abs err {err.max().item():.3e}"
+
+
+def rel(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return ((a - b).norm() / b.norm()).item()
+
+
+def make_x(M, K, seed):
+    return torch.randn(M, K, generator=gen(seed)).to(torch.bfloat16)
+
+
+def make_w(N, K, seed, std=0.02):
+    return (torch.randn(N, K, generator=gen(seed)) * std).to(torch.bfloat16)
+
+
+INT8_SHAPES = [(1, 64, 256), (3, 128, 512), (8, 192, 384), (16, 64, 1024), (17, 64, 256), (32, 512, 2560),
+               (64, 256, 640), (1, 19456, 2560), (8, 19456, 2560), (32, 19456, 2560), (64, 19456, 2560)]
+
+
+@pytest.mark.parametrize("M,N,K", INT8_SHAPES)
+def test_w8a16_gemm(M, N, K):
+    from kernels import quant_ops as ops
+    case(f"w8a16 M={M} N={N} K={K}")
+    w = make_w(N, K, 10)
+    x = make_x(M, K, 11)
+    q = O.int8_quantize(w)
+    want = O.int8_linear_fp32(x, **q)
+    y = ops.w8a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV))
+    assert y.dtype == torch.bfloat16 and y.shape == (M, N)
+    within(y, want)
+    within(O.int8_linear(x, **q), want)  # the reference's bf16 formula meets the same bound
+    assert rel(y, O.int8_linear(x, **q)) < 0.01
+
+
+def test_w8a16_fp32_scale_and_strided_x():
+    from kernels import quant_ops as ops
+    case("w8a16 fp32 scale, strided x")
+    M, N, K = 5, 256, 1024
+    w = make_w(N, K, 12)
+    xb = make_x(M, 2 * K, 13)
+    x = xb[:, K:]
+    q = O.int8_quantize(w, torch.float32)
+    want = O.int8_linear_fp32(x, **q)
+    y = ops.w8a16_linear(xb.to(DEV)[:, K:], q["qweight"].to(DEV), q["scale"].to(DEV))
+    within(y, want)
+
+
+INT4_SHAPES = [(1, 64, 256, 128), (5, 128, 512, 128), (8, 64, 1024, 256), (16, 192, 384, 128),
+               (33, 64, 512, 128), (64, 128, 768, 128), (1, 2560, 9728, 128), (8, 2560, 9728, 128),
+               (32, 2560, 9728, 128), (64, 2560, 9728, 128)]
+
+
+@pytest.mark.parametrize("M,N,K,group", INT4_SHAPES)
+@pytest.mark.parametrize("symmetric", [False, True])
+def test_w4a16_gemm(M, N, K, group, symmetric):
+    from kernels import quant_ops as ops
+    case(f"w4a16 M={M} N={N} K={K} g={group} sym={symmetric}")
+    w = make_w(N, K, 20)
+    x = make_x(M, K, 21)
+    q = O.int4_quantize_symmetric(w, group) if symmetric else O.int4_quantize(w, group)
+    want = O.int4_linear_fp32(x, **q)
+    y = ops.w4a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV),
+                         None if symmetric else q["zero"].to(DEV))
+    assert y.dtype == torch.bfloat16 and y.shape == (M, N)
+    within(y, want)
+    ref = O.int4_linear(x, **q)
+    assert rel(ref, want) < 0.01 and rel(y, ref) < 0.01
+
+
+def test_split_k_repeated_calls_are_identical():
+    """The split-K counters are left at zero: back-to-back calls give identical bytes."""
+    from kernels import quant_ops as ops
+    case("w4a16 repeated split-K calls")
+    w = make_w(2560, 9728, 30)
+    q = O.int4_quantize(w, 128)
+    qd = {k: v.to(DEV) for k, v in q.items()}
+    outs = []
+    for M in (1, 8, 1, 8):
+        x = make_x(M, 9728, 31).to(DEV)
+        outs.append(ops.w4a16_linear(x, qd["qweight"], qd["scale"], qd["zero"]).cpu())
+    assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])
+
+
+@pytest.mark.parametrize("name", ["int8_wo", "int4_wo", "fp8"])
+def test_methods_linear_matches_dequantized_matmul(name):
+    """reference tests/test_quantizaton.py:60-72 on the device, incl. the prefill branch."""
+    from engine.quantization import get_method
+    case(f"method {name}.linear")
+    m = get_method(name, device=DEV, compute_dtype=torch.bfloat16, group_size=128)
+    w = make_w(256, 512, 40).to(DEV)
+    for shape in ((2, 5, 512), (1, 512), (96, 512)):
+        x = torch.randn(*shape, generator=gen(41)).to(torch.bfloat16).to(DEV)
+        q = m.quantize(w)
+        expected = torch.nn.functional.linear(x.float(), m.dequantize(**q).float())
+        got = m.linear(x, **q)
+        assert got.shape == shape[:-1] + (256,) and got.dtype == torch.bfloat16
+        err = ((got.float() - expected).norm() / expected.norm()).item()
+        assert err < (0.05 if name == "fp8" else 0.01), (shape, err)
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 128, 128), (256, 384, 512), (200, 136, 384), (2048, 6144, 2560),
+                                   (1024, 1920, 2560), (7, 64, 256)])
+def test_fp8_gemm(M, N, K):
+    from kernels import quant_ops as ops
+    case(f"fp8 gemm M={M} N={N} K={K}")
+    x = torch.randn(M, K, generator=gen(50)).to(torch.bfloat16)
+    w = make_w(N, K, 51)
+    xq, xs = O.fp8_quantize_activation(x)
+    wq = O.fp8_quantize(w)
+    want = O.fp8_scaled_mm(xq, xs, **wq)
+    y = ops.fp8_gemm(xq.to(DEV), xs.to(DEV), wq["qweight"].to(DEV), wq["scale"].to(DEV))
+    within(y, want)
+
+
+def test_fp8_linear_end_to_end():
+    """FP8WeightAct.linear (activation quant kernel + MFMA GEMM) vs the oracle's formula
+    (fp8.py:48-61) and the emulation bound of reference tests/test_quantizaton.py:75-88."""
+    from engine.quantization import get_method
+    case("fp8 linear end to end")
+    m = get_method("fp8", device=DEV)
+    w = make_w(6144, 2560, 52)
+    x = torch.randn(64, 2560, generator=gen(53)).to(torch.bfloat16)
+    q = m.quantize(w.to(DEV))
+    y = m.linear(x.to(DEV), **q)
+    wq = O.fp8_quantize(w)
+    xq, xs = O.fp8_quantize_activation(x)
+    within(y, O.fp8_scaled_mm(xq, xs, **wq))
+    emu = O.fp8_linear_emulated(x, **wq)
+    assert ((y.float().cpu() - emu.float()).norm() / emu.float().norm()).item() < 0.02
