@@ -47,7 +47,7 @@ fp8_gemm_kernel(const uint8_t* __restrict__ A, const float* __restrict__ sa,
                 int tiles_n, int xcd_panels) {
   using C = Fp8Cfg<BM, BN, WM, WN>;
   extern __shared__ __align__(16) uint8_t smem[];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wv / WN, wn = wv - wm * WN;
 
   // Tile order: consecutive workgroups go to different XCDs (round robin), so give each
@@ -66,28 +66,24 @@ fp8_gemm_kernel(const uint8_t* __restrict__ A, const float* __restrict__ sa,
   }
   const int m0 = tm * BM, n0 = tn * BN;
 
-  // global -> register staging assignment
-  uint4 stage[C::kLoads];
-  const uint8_t* src[C::kLoads];
-  int dst[C::kLoads];
+  // global -> register staging: each thread moves kLoadsA 16-byte pieces of the A tile and
+  // kLoadsB of the B tile per k-step (the configurations divide exactly, so no guards and
+  // every array index is a compile-time constant after unrolling)
+  static_assert((BM * 8) % C::kThreads == 0 && (BN * 8) % C::kThreads == 0, "tile / thread mismatch");
+  constexpr int kLoadsA = BM * 8 / C::kThreads, kLoadsB = BN * 8 / C::kThreads;
+  const int c16 = (tid & 7) * 16;
+  const int row_step = C::kThreads / 8;
+  const uint8_t* srcA = A + (int64_t)min(m0 + (tid >> 3), M - 1) * K + c16;
+  const uint8_t* srcB = B + (int64_t)min(n0 + (tid >> 3), N - 1) * K + c16;
+  int64_t offA[kLoadsA], offB[kLoadsB];
 #pragma unroll
-  for (int j = 0; j < C::kLoads; ++j) {
-    const int i = tid + j * C::kThreads;
-    const int row = i >> 3, c = i & 7;  // 8 pieces of 16 bytes per 128-byte row
-    if (i < C::kPieces) {
-      if (row < BM) {
-        const int gm = min(m0 + row, M - 1);
-        src[j] = A + (int64_t)gm * K + c * 16;
-      } else {
-        const int gn = min(n0 + row - BM, N - 1);
-        src[j] = B + (int64_t)gn * K + c * 16;
-      }
-      dst[j] = row * LDS_ROW + c * 16;
-    } else {
-      src[j] = A;
-      dst[j] = -1;
-    }
-  }
+  for (int j = 0; j < kLoadsA; ++j)
+    offA[j] = (int64_t)(min(m0 + (tid >> 3) + j * row_step, M - 1) - min(m0 + (tid >> 3), M - 1)) * K;
+#pragma unroll
+  for (int j = 0; j < kLoadsB; ++j)
+    offB[j] = (int64_t)(min(n0 + (tid >> 3) + j * row_step, N - 1) - min(n0 + (tid >> 3), N - 1)) * K;
+  const int dst0 = (tid >> 3) * LDS_ROW + c16;
+  uint4 ra[kLoadsA], rb[kLoadsB];
 
   f32x4 acc[C::kTM][C::kTN];
 #pragma unroll
@@ -98,11 +94,13 @@ fp8_gemm_kernel(const uint8_t* __restrict__ A, const float* __restrict__ sa,
   const int nsteps = K / BK;
   // prologue: step 0 -> buffer 0
 #pragma unroll
-  for (int j = 0; j < C::kLoads; ++j)
-    if (dst[j] >= 0) stage[j] = *reinterpret_cast<const uint4*>(src[j]);
+  for (int j = 0; j < kLoadsA; ++j) ra[j] = *reinterpret_cast<const uint4*>(srcA + offA[j]);
 #pragma unroll
-  for (int j = 0; j < C::kLoads; ++j)
-    if (dst[j] >= 0) *reinterpret_cast<uint4*>(smem + dst[j]) = stage[j];
+  for (int j = 0; j < kLoadsB; ++j) rb[j] = *reinterpret_cast<const uint4*>(srcB + offB[j]);
+#pragma unroll
+  for (int j = 0; j < kLoadsA; ++j) *reinterpret_cast<uint4*>(smem + dst0 + j * row_step * LDS_ROW) = ra[j];
+#pragma unroll
+  for (int j = 0; j < kLoadsB; ++j) *reinterpret_cast<uint4*>(smem + (BM + j * row_step) * LDS_ROW + dst0) = rb[j];
   __syncthreads();
 
   const int fr = lane & 15, fk = (lane >> 4) * 32;
@@ -110,11 +108,11 @@ fp8_gemm_kernel(const uint8_t* __restrict__ A, const float* __restrict__ sa,
     uint8_t* cur = smem + (s & 1) * (BM + BN) * LDS_ROW;
     uint8_t* nxt = smem + ((s + 1) & 1) * (BM + BN) * LDS_ROW;
     const bool more = s + 1 < nsteps;
-    if (more) {
+    const int64_t kn = (int64_t)(more ? s + 1 : s) * BK;  // the last step re-reads (unused)
 #pragma unroll
-      for (int j = 0; j < C::kLoads; ++j)
-        if (dst[j] >= 0) stage[j] = *reinterpret_cast<const uint4*>(src[j] + (int64_t)(s + 1) * BK);
-    }
+    for (int j = 0; j < kLoadsA; ++j) ra[j] = *reinterpret_cast<const uint4*>(srcA + offA[j] + kn);
+#pragma unroll
+    for (int j = 0; j < kLoadsB; ++j) rb[j] = *reinterpret_cast<const uint4*>(srcB + offB[j] + kn);
     i32x8 bfr[C::kTN];
 #pragma unroll
     for (int j = 0; j < C::kTN; ++j) {
@@ -134,8 +132,9 @@ fp8_gemm_kernel(const uint8_t* __restrict__ A, const float* __restrict__ sa,
     }
     if (more) {
 #pragma unroll
-      for (int j = 0; j < C::kLoads; ++j)
-        if (dst[j] >= 0) *reinterpret_cast<uint4*>(nxt + dst[j]) = stage[j];
+      for (int j = 0; j < kLoadsA; ++j) *reinterpret_cast<uint4*>(nxt + dst0 + j * row_step * LDS_ROW) = ra[j];
+#pragma unroll
+      for (int j = 0; j < kLoadsB; ++j) *reinterpret_cast<uint4*>(nxt + (BM + j * row_step) * LDS_ROW + dst0) = rb[j];
     }
     __syncthreads();
   }

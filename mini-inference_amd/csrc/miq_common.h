@@ -81,6 +81,23 @@ __host__ __device__ inline uint8_t f32_to_fp8(float x) {
   return static_cast<uint8_t>(sign | code);
 }
 
+// Raw bits of element i of a bf16 / f16 / f32 array (SD = the MIQ_* dtype). The value is
+// decoded by sd_to_f32 where it is used, so a pending load never forces a wait where it
+// is issued (a decode inside a dtype branch would make the compiler wait for all
+// outstanding loads right there).
+template <int SD>
+__device__ inline uint32_t load_sd_raw(const void* p, int64_t i) {
+  if constexpr (SD == MIQ_F32) return static_cast<const uint32_t*>(p)[i];
+  else return static_cast<const uint16_t*>(p)[i];
+}
+
+template <int SD>
+__device__ inline float sd_to_f32(uint32_t raw) {
+  if constexpr (SD == MIQ_F32) return __builtin_bit_cast(float, raw);
+  else if constexpr (SD == MIQ_BF16) return __builtin_bit_cast(float, raw << 16);
+  else return f16_to_f32(static_cast<uint16_t>(raw));
+}
+
 __device__ inline float load_scalar(const void* p, int dtype, int64_t i) {
   switch (dtype) {
     case MIQ_BF16: return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);

@@ -31,7 +31,7 @@ moe_align_kernel(const void* __restrict__ ids, int dtype, int num_pairs, int E, 
   extern __shared__ int sm[];
   int* counts = sm;               // [E]
   int* offsets = sm + E;          // [E + 1]
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), nw = blockDim.x >> 6;
   for (int e = tid; e < E; e += blockDim.x) counts[e] = 0;
   __syncthreads();
   for (int i = tid; i < num_pairs; i += blockDim.x) {
@@ -113,8 +113,53 @@ __device__ inline void stage_rows(const uint16_t* base, int64_t ld, const int* s
 
 __device__ inline float bf16r(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// Stream all k-steps of one 16-row weight tile (row `row` of lane r) against the
+// staged activation rows; returns the tile's 16x16 result in C layout.
+template <bool HZ, int SD>
+__device__ inline f32x4 tile_product(const MoeParams& p, const uint8_t* wbase, int64_t row, int K,
+                                     const void* sc, const void* zr, const uint16_t* src, int64_t ld,
+                                     const int* src_row, uint16_t* lds, int chunk_steps, int r, int g,
+                                     const int64_t (&tile_rows)[4], int wv) {
+  const uint8_t* wrow[1] = {wbase + row * (K / 2)};
+  f32x4 acc[1][1], accg[1][1];
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  acc[0][0] = z4;
+  accg[0][0] = z4;
+  const int lds_stride = chunk_steps * kStepK + 8;
+  const int steps = K / kStepK;
+  const int ngroups = steps / p.group_steps;
+  // LDS: [activation chunk][activation sums per group][scales of the 4 wavefronts'
+  // 16-row tiles][zeros]
+  float* xsum = reinterpret_cast<float*>(lds + kTile * lds_stride);
+  typedef typename GroupQ<SD>::raw_t raw_t;
+  raw_t* lsc = reinterpret_cast<raw_t*>(xsum + ngroups * kTile);
+  raw_t* lzr = lsc + 64 * ngroups;
+  const GroupQ<SD> q{lsc + wv * 16 * ngroups, HZ ? lzr + wv * 16 * ngroups : nullptr, ngroups, 0, p.group_steps,
+                     xsum, kTile};
+  for (int i = threadIdx.x; i < ngroups * kTile; i += blockDim.x) xsum[i] = 0.f;
+  for (int c0 = 0; c0 < steps; c0 += chunk_steps) {
+    const int c1 = min(steps, c0 + chunk_steps);
+    Batch<KIND_INT4, 1, 16> bt;
+    load_batch<KIND_INT4, 1, 16>(wrow, bt, c0, c1, g);  // in flight during staging
+    if (c0) __syncthreads();
+    stage_rows(src, ld, src_row, lds, lds_stride, c0, c1 - c0);
+    if (c0 == 0) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        stage_groups<SD>(sc, ngroups, tile_rows[w], 16, 0, ngroups, lsc + w * 16 * ngroups);
+        if (HZ) stage_groups<SD>(zr, ngroups, tile_rows[w], 16, 0, ngroups, lzr + w * 16 * ngroups);
+      }
+    }
+    __syncthreads();
+    sum_activations(lds, lds_stride, kTile, c1 - c0, c0, p.group_steps, 0, true, xsum, kTile);
+    __syncthreads();
+    stream_steps<KIND_INT4, 1, 1, HZ, SD, 16>(q, kTile, wrow, bt, lds, lds_stride, c0, c1, c0, r, g, acc, accg);
+  }
+  return acc[0][0];
+}
+
 // gate/up: workgroup = (32 columns of I, one tile); waves 0-1 gate rows, 2-3 up rows
-template <bool HZ>
+template <bool HZ, int SD>
 __global__ void __launch_bounds__(256)
 moe_gate_up_kernel(MoeParams p, int chunk_steps) {
   extern __shared__ __align__(16) uint16_t lds[];
@@ -123,31 +168,20 @@ moe_gate_up_kernel(MoeParams p, int chunk_steps) {
   const int tile = blockIdx.y;
   if (tile * kTile >= *p.num_padded) return;
   const int e = p.expert_ids[tile];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r = lane & 15, g = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), r = lane & 15, g = lane >> 4;
   if (tid < kTile) {
     const int pair = p.sorted_ids[tile * kTile + tid];
     s_src[tid] = pair < p.num_pairs ? pair / p.topk : -1;
   }
-  const int n0 = blockIdx.x * 32;
-  const int wrow_idx = (wv < 2 ? 0 : p.I) + n0 + (wv & 1) * 16 + r;  // row of gate_up[e]
-  const int64_t row = (int64_t)e * 2 * p.I + wrow_idx;
-  const uint8_t* wrow = p.gu_q + row * (p.H / 2);
-  const int ngroups = p.H / (p.group_steps * kStepK);
-  GroupScales gs{p.gu_s, p.gu_z, p.sz_dtype, p.group_steps, row * ngroups};
-  Acc<1> st;
-  st.clear();
-  const int lds_stride = chunk_steps * kStepK + 8;
-  const int steps = p.H / kStepK;
   __syncthreads();
-  for (int c0 = 0; c0 < steps; c0 += chunk_steps) {
-    const int ns = min(chunk_steps, steps - c0);
-    if (c0) __syncthreads();
-    stage_rows(p.hidden, p.H, s_src, lds, lds_stride, c0, ns);
-    __syncthreads();
-    run_steps<KIND_INT4, 1, HZ>(wrow, lds, lds_stride, kTile, c0, ns, r, g, gs, st);
-  }
+  const int n0 = blockIdx.x * 32;
+  const int64_t base = (int64_t)e * 2 * p.I + n0;
+  const int64_t tile_rows[4] = {base, base + 16, base + p.I, base + p.I + 16};
+  const int64_t row = tile_rows[wv] + r;
+  const f32x4 acc = tile_product<HZ, SD>(p, p.gu_q, row, p.H, p.gu_s, p.gu_z, p.hidden, p.H, s_src, lds,
+                                         chunk_steps, r, g, tile_rows, wv);
 #pragma unroll
-  for (int v = 0; v < 4; ++v) s_gu[wv][g * 4 + v][r] = st.acc[0][v];
+  for (int v = 0; v < 4; ++v) s_gu[wv][g * 4 + v][r] = acc[v];
   __syncthreads();
   // h[m][c] = silu(gate) * up with the reference's bf16 roundings, c in [0, 32)
   for (int i = tid; i < kTile * 32; i += 256) {
@@ -160,7 +194,7 @@ moe_gate_up_kernel(MoeParams p, int chunk_steps) {
 }
 
 // down: workgroup = (64 columns of H, one tile)
-template <bool HZ>
+template <bool HZ, int SD>
 __global__ void __launch_bounds__(256)
 moe_down_kernel(MoeParams p, int chunk_steps) {
   extern __shared__ __align__(16) uint16_t lds[];
@@ -168,35 +202,25 @@ moe_down_kernel(MoeParams p, int chunk_steps) {
   const int tile = blockIdx.y;
   if (tile * kTile >= *p.num_padded) return;
   const int e = p.expert_ids[tile];
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, r = lane & 15, g = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), r = lane & 15, g = lane >> 4;
   if (tid < kTile) {
     const int pair = p.sorted_ids[tile * kTile + tid];
     s_src[tid] = pair < p.num_pairs ? tile * kTile + tid : -1;
   }
-  const int n = blockIdx.x * 64 + wv * 16 + r;
-  const int64_t row = (int64_t)e * p.H + n;
-  const uint8_t* wrow = p.dn_q + row * (p.I / 2);
-  const int ngroups = p.I / (p.group_steps * kStepK);
-  GroupScales gs{p.dn_s, p.dn_z, p.sz_dtype, p.group_steps, row * ngroups};
-  Acc<1> st;
-  st.clear();
-  const int lds_stride = chunk_steps * kStepK + 8;
-  const int steps = p.I / kStepK;
   __syncthreads();
-  for (int c0 = 0; c0 < steps; c0 += chunk_steps) {
-    const int ns = min(chunk_steps, steps - c0);
-    if (c0) __syncthreads();
-    stage_rows(p.hbuf, p.I, s_src, lds, lds_stride, c0, ns);
-    __syncthreads();
-    run_steps<KIND_INT4, 1, HZ>(wrow, lds, lds_stride, kTile, c0, ns, r, g, gs, st);
-  }
+  const int n = blockIdx.x * 64 + wv * 16 + r;
+  const int64_t base = (int64_t)e * p.H + blockIdx.x * 64;
+  const int64_t tile_rows[4] = {base, base + 16, base + 32, base + 48};
+  const int64_t row = base + wv * 16 + r;
+  const f32x4 acc = tile_product<HZ, SD>(p, p.dn_q, row, p.I, p.dn_s, p.dn_z, p.hbuf, p.I, s_src, lds,
+                                         chunk_steps, r, g, tile_rows, wv);
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int m = g * 4 + v;
     const int pair = p.sorted_ids[tile * kTile + m];
     if (pair < p.num_pairs) {
       const float w = bf16_to_f32(p.topk_w[pair]);
-      p.ypair[(int64_t)pair * p.H + n] = bf16r(bf16r(st.acc[0][v]) * w);
+      p.ypair[(int64_t)pair * p.H + n] = bf16r(bf16r(acc[v]) * w);
     }
   }
 }
@@ -209,6 +233,28 @@ __global__ void moe_combine_kernel(const float* __restrict__ ypair, int topk, in
   float s = 0.f;
   for (int j = 0; j < topk; ++j) s += ypair[((int64_t)t * topk + j) * H + n];
   out[(int64_t)t * H + n] = f32_to_bf16(s);
+}
+
+template <bool HZ, int SD>
+void launch_experts_t(const MoeParams& p, dim3 gu_grid, dim3 dn_grid, int gu_chunk, int dn_chunk, size_t gu_lds,
+                      size_t dn_lds, hipStream_t st) {
+  hipLaunchKernelGGL((moe_gate_up_kernel<HZ, SD>), gu_grid, dim3(256), gu_lds, st, p, gu_chunk);
+  hipLaunchKernelGGL((moe_down_kernel<HZ, SD>), dn_grid, dim3(256), dn_lds, st, p, dn_chunk);
+}
+
+void launch_experts(const MoeParams& p, bool hz, int sd, dim3 gu_grid, dim3 dn_grid, int gu_chunk, int dn_chunk,
+                    size_t gu_lds, size_t dn_lds, hipStream_t st) {
+#define MIQ_EXPERTS(HZV, SDV) launch_experts_t<HZV, SDV>(p, gu_grid, dn_grid, gu_chunk, dn_chunk, gu_lds, dn_lds, st)
+  if (hz) {
+    if (sd == MIQ_BF16) MIQ_EXPERTS(true, MIQ_BF16);
+    else if (sd == MIQ_F16) MIQ_EXPERTS(true, MIQ_F16);
+    else MIQ_EXPERTS(true, MIQ_F32);
+  } else {
+    if (sd == MIQ_BF16) MIQ_EXPERTS(false, MIQ_BF16);
+    else if (sd == MIQ_F16) MIQ_EXPERTS(false, MIQ_F16);
+    else MIQ_EXPERTS(false, MIQ_F32);
+  }
+#undef MIQ_EXPERTS
 }
 
 size_t max_padded_rows(int64_t num_pairs, int64_t E) { return (size_t)(num_pairs + E * (kTile - 1)); }
@@ -286,15 +332,13 @@ extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I
   // LDS chunk: 16 rows x up to 1024 k (32 KiB)
   const int gu_chunk = (int)std::min<int64_t>(8, H / kStepK);
   const int dn_chunk = (int)std::min<int64_t>(8, I / kStepK);
-  const size_t gu_lds = (size_t)kTile * (gu_chunk * kStepK + 8) * 2;
-  const size_t dn_lds = (size_t)kTile * (dn_chunk * kStepK + 8) * 2;
-  if (gu_zero) hipLaunchKernelGGL(moe_gate_up_kernel<true>, dim3((unsigned)(I / 32), tiles), dim3(256), gu_lds, st, p, gu_chunk);
-  else hipLaunchKernelGGL(moe_gate_up_kernel<false>, dim3((unsigned)(I / 32), tiles), dim3(256), gu_lds, st, p, gu_chunk);
-  int rc = check_launch("w4a16_moe gate_up");
-  if (rc) return rc;
-  if (dn_zero) hipLaunchKernelGGL(moe_down_kernel<true>, dim3((unsigned)(H / 64), tiles), dim3(256), dn_lds, st, p, dn_chunk);
-  else hipLaunchKernelGGL(moe_down_kernel<false>, dim3((unsigned)(H / 64), tiles), dim3(256), dn_lds, st, p, dn_chunk);
-  rc = check_launch("w4a16_moe down");
+  const size_t gu_lds = (size_t)kTile * (gu_chunk * kStepK + 8) * 2 + (size_t)64 * (H / group) * 4 * 2 +
+                        (size_t)kTile * (H / group) * 4;
+  const size_t dn_lds = (size_t)kTile * (dn_chunk * kStepK + 8) * 2 + (size_t)64 * (I / group) * 4 * 2 +
+                        (size_t)kTile * (I / group) * 4;
+  const dim3 gu_grid((unsigned)(I / 32), tiles), dn_grid((unsigned)(H / 64), tiles);
+  launch_experts(p, gu_zero != nullptr, sz_dtype, gu_grid, dn_grid, gu_chunk, dn_chunk, gu_lds, dn_lds, st);
+  int rc = check_launch("w4a16_moe experts");
   if (rc) return rc;
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)T), dim3(256), 0, st,
                      p.ypair, (int)topk, (int)H, p.out);

@@ -102,14 +102,14 @@ __device__ inline float sum16(float v) {
   return v;
 }
 
-template <int KVT, bool HAS_SCALE>
+template <int KVT, bool HAS_SCALE, int SD>
 __global__ void __launch_bounds__(kWaves * 64)
 paged_decode_split_kernel(AttnParams p) {
   const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int L = p.lens[b];
   const int p0 = part * p.partition;
   if (part > 0 && p0 >= L) return;  // partition beyond this request's context
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
   const int GROUP = p.group;
 
@@ -180,8 +180,9 @@ paged_decode_split_kernel(AttnParams p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) s4 = mfma16(qf[j], kf[j], s4);
       // C layout: lane holds heads 4 * g + v of token column r
-      float kscale = qk_scale;
-      if (HAS_SCALE) kscale *= load_scalar(p.ks, p.s_dtype, slot * p.ss_t + (int64_t)kvh * p.ss_h);
+      uint32_t kraw = 0;
+      if (HAS_SCALE) kraw = load_sd_raw<SD>(p.ks, slot * p.ss_t + (int64_t)kvh * p.ss_h);
+      const float kscale = HAS_SCALE ? qk_scale * sd_to_f32<SD>(kraw) : qk_scale;
 #pragma unroll
       for (int v = 0; v < 4; ++v) sc[c][v] = valid ? s4[v] * kscale : -__builtin_inff();
     }
@@ -208,7 +209,7 @@ paged_decode_split_kernel(AttnParams p) {
       if (HAS_SCALE) {
         const int tc = t < t_end ? t : t_end - 1;
         const int64_t slot = (int64_t)p.bt[(int64_t)b * p.bt_stride + tc / p.page] * p.page + tc % p.page;
-        vsc = load_scalar(p.vs, p.s_dtype, slot * p.ss_t + (int64_t)kvh * p.ss_h);
+        vsc = sd_to_f32<SD>(load_sd_raw<SD>(p.vs, slot * p.ss_t + (int64_t)kvh * p.ss_h));
       }
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
@@ -340,9 +341,17 @@ paged_decode_merge_kernel(const float* __restrict__ o_part, const float* __restr
   out[(int64_t)b * os_b + (int64_t)h * os_h + d] = f32_to_bf16(den > 0.f ? num / den : 0.f);
 }
 
+template <int KVT, bool HS, int SD>
+void launch_split3(const AttnParams& p, dim3 grid, hipStream_t st) {
+  hipLaunchKernelGGL((paged_decode_split_kernel<KVT, HS, SD>), grid, dim3(kWaves * 64), 0, st, p);
+}
+
 template <int KVT, bool HS>
 void launch_split(const AttnParams& p, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((paged_decode_split_kernel<KVT, HS>), grid, dim3(kWaves * 64), 0, st, p);
+  if (!HS) launch_split3<KVT, HS, MIQ_F32>(p, grid, st);
+  else if (p.s_dtype == MIQ_BF16) launch_split3<KVT, HS, MIQ_BF16>(p, grid, st);
+  else if (p.s_dtype == MIQ_F16) launch_split3<KVT, HS, MIQ_F16>(p, grid, st);
+  else launch_split3<KVT, HS, MIQ_F32>(p, grid, st);
 }
 
 }  // namespace

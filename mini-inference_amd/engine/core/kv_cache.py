@@ -45,6 +45,20 @@ def tokens_for_budget(budget_bytes, num_layers, num_kv_heads, head_dim, dtype, k
     return int(budget_bytes // kv_bytes_per_token(num_layers, num_kv_heads, head_dim, dtype, kv_dtype))
 
 
+def kv_quant_write(cache, scale, slots, x):
+    """Quantize x [T, heads, D] per (token, head) into the 8-bit `cache` [slots, heads, D]
+    at rows `slots` (int64), scales into `scale` [slots, heads] (kv_cache.py:359-388)."""
+    L.require_device(x, slots, cache, scale)
+    x = x if x.stride(-1) == 1 else x.contiguous()
+    T = x.shape[0]
+    for a in range(0, T, 65535):  # the kernel takes at most 65535 tokens per launch
+        xa, sa = x[a:a + 65535], slots[a:a + 65535]
+        L.call("miq_kv_quant_write", L.ptr(xa), L.dtype_code(xa.dtype), xa.shape[0], xa.shape[1], xa.shape[2],
+               xa.stride(0), xa.stride(1), L.ptr(sa), L.ptr(cache), L.dtype_code(cache.dtype),
+               cache.stride(0), cache.stride(1), L.ptr(scale), L.dtype_code(scale.dtype),
+               scale.stride(0), scale.stride(1), L.stream(x.device))
+
+
 class KVCache:
     """Storage of a paged KV cache (kv_cache.py:305-333). `mode` must be "paged"."""
 
@@ -71,14 +85,6 @@ class KVCache:
             self.v_scale = torch.ones(shape[:3], dtype=dtype, device=device)
         self.bytes_per_token = kv_bytes_per_token(num_layers, num_kv_heads, head_dim, dtype, self.kv_dtype)
 
-    def _write_one(self, cache, scale, slots, x):
-        L.require_device(x, slots, cache)
-        x = x if x.stride(-1) == 1 else x.contiguous()
-        L.call("miq_kv_quant_write", L.ptr(x), L.dtype_code(x.dtype), x.shape[0], x.shape[1], x.shape[2],
-               x.stride(0), x.stride(1), L.ptr(slots), L.ptr(cache), L.dtype_code(cache.dtype),
-               cache.stride(0), cache.stride(1), L.ptr(scale), L.dtype_code(scale.dtype),
-               scale.stride(0), scale.stride(1), L.stream(x.device))
-
     def write(self, layer, slots, k, v):
         """kv_cache.py:378-388: quantize k, v [T, heads, D] and store them at `slots`."""
         if self.kv_dtype is None:
@@ -86,8 +92,8 @@ class KVCache:
             self.v[layer].index_copy_(0, slots, v)
             return
         slots = slots.to(torch.int64).contiguous()
-        self._write_one(self.k[layer], self.k_scale[layer], slots, k)
-        self._write_one(self.v[layer], self.v_scale[layer], slots, v)
+        kv_quant_write(self.k[layer], self.k_scale[layer], slots, k)
+        kv_quant_write(self.v[layer], self.v_scale[layer], slots, v)
 
     def gather(self, layer, idx):
         """kv_cache.py:390-401: keys and values at the given slots, in the model dtype."""
