@@ -1,0 +1,474 @@
+// Weight-only quantized skinny GEMM (1 <= M <= 64) for gfx950:
+//
+//   y[m, n] = sum_k x[m, k] * W[n, k],  x bf16 [M, K],  W int8 [N, K] or int4 [N, K/2]
+//
+// Work decomposition:
+//   * a workgroup of 4 wavefronts owns a row block of 4 * NR tiles of 16 weight rows and
+//     a K range (one of S splits along grid.y); wavefront w owns tiles w * NR .. + NR - 1
+//     over the whole range, so the activations it multiplies are shared by the 4
+//     wavefronts through LDS (x is read from L2 once per row block, not once per tile);
+//   * the activations of a chunk of the range are staged in LDS by a short loop; while a
+//     thread writes its pieces it also adds their 8 values, and a 16-lane DPP reduction
+//     gives sum_k x over every k-step, which removes the +128 code offset (below) with 4
+//     FMAs per group instead of one MFMA per operand;
+//   * weights stream through a ring of D k-steps of registers: step k + D is requested
+//     (16-byte non-temporal buffer loads, one per lane) right after step k has been
+//     multiplied, so D steps are always in flight and the wait before a step is a
+//     constant count. Requests past the range use an offset outside the buffer, which
+//     the hardware answers with zeros without touching memory;
+//   * the code is a pair of short loops: these kernels run for a few microseconds, and
+//     the instruction fetch of straight-line code costs about as much as the loads;
+//   * with S > 1 every workgroup publishes fp32 partials with agent-coherent (sc1)
+//     stores, waits for them and bumps a per-row-block arrival counter; the last one adds
+//     the S partials in split order (deterministic), writes bf16 and resets the counter.
+//
+// Unpacking: a 4-bit code u becomes the bf16 value 128 + u with one AND-OR per pair
+// (0x4300 | u == 128 + u, exact) and an int8 code q becomes 128 + q via xor + byte
+// convert. The MFMA yields sum x * (128 + u); then per group (int4)
+//   acc += scale * sum x (128 + u) + (zero - 128 scale) * sum x     (asymmetric)
+//   acc += scale * sum x (128 + u) - 136 scale * sum x              (symmetric, u - 8)
+// and per row (int8) y = bf16(bf16(sum x (128 + q) - 128 sum x) * bf16(scale)).
+#include <stdio.h>
+#include <stdlib.h>
+
+#include "wo_core.h"
+
+#ifndef MIQ_TRACE
+#define MIQ_TRACE(point)
+#endif
+
+namespace miq {
+namespace {
+
+using namespace wo;
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+constexpr int kMaxCounters = 4096;   // row blocks that may use split-K
+constexpr int kCounterBytes = kMaxCounters * 4;
+
+// Compile-time shape of one instantiation: MT tiles of 16 activation rows, NR weight
+// tiles per wavefront, D k-steps of weights in flight per wavefront (8 KiB).
+template <int KIND, int MT, int NR>
+struct Cfg {
+  static constexpr int NL = KIND == KIND_INT4 ? 1 : 2;       // 16-byte loads per tile-step
+  static constexpr int D = (KIND == KIND_INT4 ? 8 : 4) / NR;  // ring depth in k-steps
+  static constexpr int XR = 16 * MT;                          // x-sum row pitch
+  static constexpr int XP = 4;                                // staging pieces per thread per round
+};
+
+struct StreamParams {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint8_t* w;
+  int64_t ldw;          // bytes per weight row
+  const void* scale;
+  const void* zero;
+  int group_steps;      // int4: k-steps per quantization group (1 for int8)
+  int64_t ngroups;      // int4: groups per weight row
+  uint16_t* y;
+  int64_t ldy;
+  int M, N;
+  int S, units, unit_steps;
+  int chunk_steps;      // k-steps of x staged in LDS at once (a multiple of D)
+  int wbytes, sbytes;   // sizes of the weight and scale / zero buffers
+  float* partial;       // [S][M][N]
+  int* counters;        // [kMaxCounters]
+};
+
+__device__ inline float sum8_bf16(uint4 v) {
+  const float lo = bf16_to_f32(v.x & 0xffff) + bf16_to_f32(v.y & 0xffff) + bf16_to_f32(v.z & 0xffff) +
+                   bf16_to_f32(v.w & 0xffff);
+  const float hi = bf16_to_f32(v.x >> 16) + bf16_to_f32(v.y >> 16) + bf16_to_f32(v.z >> 16) + bf16_to_f32(v.w >> 16);
+  return lo + hi;
+}
+
+// The aligned 32-bit word holding element i of a bf16 / f16 / f32 array (a 16-bit load
+// would be widened right where it is issued, which makes the compiler wait for it), and
+// the element's value from that word.
+template <int SD>
+__device__ inline uint32_t load_sd_word(const void* p, int64_t i) {
+  if constexpr (SD == MIQ_F32) return static_cast<const uint32_t*>(p)[i];
+  else return static_cast<const uint32_t*>(p)[i >> 1];
+}
+
+template <int SD>
+__device__ inline float word_to_f32(uint32_t w, int64_t i) {
+  if constexpr (SD == MIQ_F32) return __builtin_bit_cast(float, w);
+  else return sd_to_f32<SD>((i & 1) ? (w >> 16) : (w & 0xffffu));
+}
+
+template <int KIND, bool HZ, int SD, int MT, int NR>
+__global__ void __launch_bounds__(kThreads)
+wo_stream_kernel(StreamParams p) {
+  using C = Cfg<KIND, MT, NR>;
+  constexpr int D = C::D, NL = C::NL, XR = C::XR, XP = C::XP;
+  constexpr int kStepBytes = KIND == KIND_INT4 ? kStepK / 2 : kStepK;  // per weight row
+  extern __shared__ __align__(16) uint16_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int M = p.M;
+  MIQ_TRACE(0);
+#ifdef MIQ_TRACE_ARGS
+  asm volatile("" ::"s"(M), "s"(p.w), "s"(p.x));
+  MIQ_TRACE(5);
+#endif
+
+  // K range of this split, in whole units (k-steps for int8, groups for int4)
+  const int s = blockIdx.y;
+  const int u0 = (int)((int64_t)p.units * s / p.S), u1 = (int)((int64_t)p.units * (s + 1) / p.S);
+  const int st0 = u0 * p.unit_steps, st1 = u1 * p.unit_steps;
+
+  // this wavefront's weight rows (rows past N re-read row N - 1; never stored) and the
+  // byte offsets of their k-step st0 in the weight / scale buffers
+  const int nblk0 = blockIdx.x * (kWaves * NR * 16);
+  int nrow[NR], woff[NR], soff[NR];
+#pragma unroll
+  for (int t = 0; t < NR; ++t) {
+    nrow[t] = nblk0 + (wv * NR + t) * 16 + r;
+    const int nc = min(nrow[t], p.N - 1);
+    woff[t] = nc * (int)p.ldw + st0 * kStepBytes + g * 16;
+    soff[t] = (int)(nc * p.ngroups + st0 / p.group_steps);  // element index of the first group
+  }
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.w), 0, p.wbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.scale), 0, p.sbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t zrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(HZ ? p.zero : p.scale), 0, p.sbytes, 0x00020000);
+  constexpr int kOut = 0x7ffffff0;  // an offset outside every buffer: the load returns zeros
+
+  // ring of D k-steps: weights and (int4) the raw scale / zero word of each step's group
+  uint4 wq[D][NR][NL];
+  uint32_t sq[D][NR], zq[D][NR];
+  // steps in the range, as an opaque per-lane value: requests past it are steered to
+  // kOut with bit operations (a select would become a branch around each load, and
+  // branches cost the precise waits)
+  int nsteps_v = st1 - st0;
+  asm volatile("" : "+v"(nsteps_v));
+  auto request = [&](int d, int kl) {  // k-step st0 + kl into slot d
+    const int keep = (kl - nsteps_v) >> 31;  // all ones while kl < steps in range
+#pragma unroll
+    for (int t = 0; t < NR; ++t) {
+#pragma unroll
+      for (int L = 0; L < NL; ++L) {
+        const int off = ((woff[t] + kl * kStepBytes + L * 64) & keep) | (kOut & ~keep);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2 /* nt */);
+        wq[d][t][L] = *reinterpret_cast<const uint4*>(&v);
+      }
+      if (KIND == KIND_INT4) {
+        const int gi = soff[t] + kl / p.group_steps;
+        constexpr int esz = SD == MIQ_F32 ? 4 : 2;
+        const int so = ((gi * esz) & ~3 & keep) | (kOut & ~keep);
+        sq[d][t] = __builtin_amdgcn_raw_buffer_load_b32(srs, so, 0, 0);
+        zq[d][t] = HZ ? __builtin_amdgcn_raw_buffer_load_b32(zrs, so, 0, 0) : 0u;
+      }
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d) request(d, d);
+  MIQ_TRACE(1);
+
+  f32x4 acc[NR][MT], accg[NR][MT], xsg[MT];
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < NR; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) { acc[t][mt] = z4; accg[t][mt] = z4; }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xsg[mt] = z4;
+
+  // LDS: x chunk [M rows x (CS * 128 + 8)] bf16, then [CS][XR] fp32 sums per k-step
+  const int CS = p.chunk_steps;
+  const int xstride = CS * kStepK + 8;
+  float* xsum = reinterpret_cast<float*>(lds + M * xstride);
+  const int xld = (int)(p.ldx / 8);
+
+  for (int c0 = st0; c0 < st1; c0 += CS) {
+    const int nst = min(CS, st1 - c0);
+    const int xcols = nst * (kStepK / 8);  // 16-byte pieces per activation row
+    const int npieces = M * xcols;
+    const uint4* xsrc = reinterpret_cast<const uint4*>(p.x) + (int64_t)c0 * (kStepK / 8);
+    if (c0 != st0) __syncthreads();  // every wavefront is done with the previous chunk
+    for (int base = 0; base < npieces; base += XP * kThreads) {
+      uint4 xr[XP];
+#pragma unroll
+      for (int j = 0; j < XP; ++j) {
+        const int i = min(base + tid + j * kThreads, npieces - 1);
+        const int m = i / xcols, c = i - m * xcols;
+        xr[j] = xsrc[(int64_t)m * xld + c];
+      }
+#pragma unroll
+      for (int j = 0; j < XP; ++j) {
+        const int i = base + tid + j * kThreads;
+        const int ic = min(i, npieces - 1);
+        const int m = ic / xcols, c = ic - m * xcols;
+        *reinterpret_cast<uint4*>(lds + m * xstride + c * 8) = KIND == KIND_INT4 ? permute_for_u4(xr[j]) : xr[j];
+        // sum over the 16 pieces of one k-step (16 consecutive lanes, one DPP row):
+        // lane 15 of the row ends with the total
+        float sm = sum8_bf16(xr[j]);
+        sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x111, 0xf, 0xf, true));
+        sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x112, 0xf, 0xf, true));
+        sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x114, 0xf, 0xf, true));
+        sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x118, 0xf, 0xf, true));
+        if (i < npieces && (c & 15) == 15) xsum[(c >> 4) * XR + m] = sm;
+      }
+    }
+    __syncthreads();
+    if (c0 == st0) MIQ_TRACE(2);
+
+    // multiply the chunk, D k-steps per trip; the ring slot of step kl is kl % D
+    for (int k = c0; k < c0 + nst; k += D) {
+#pragma unroll
+      for (int d = 0; d < D; ++d) {
+        const int kst = k + d, kl = kst - c0;
+        if (kst < c0 + nst) {
+          bf16x8 av[MT][4];
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const uint16_t* row = lds + min(mt * 16 + r, M - 1) * xstride;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint4 v = *reinterpret_cast<const uint4*>(row + a_off<KIND>(kl, g, j));
+              av[mt][j] = as_bf16x8(v.x, v.y, v.z, v.w);
+            }
+            xsg[mt] += *reinterpret_cast<const f32x4*>(xsum + kl * XR + mt * 16 + g * 4);
+          }
+#pragma unroll
+          for (int t = 0; t < NR; ++t) {
+            bf16x8 bv[4];
+            unpack_b<KIND>(wq[d][t], bv);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                if (KIND == KIND_INT4) accg[t][mt] = mfma(av[mt][j], bv[j], accg[t][mt]);
+                else acc[t][mt] = mfma(av[mt][j], bv[j], acc[t][mt]);
+              }
+          }
+          if (KIND == KIND_INT4 && (kst + 1) % p.group_steps == 0) {  // end of a quantization group
+#pragma unroll
+            for (int t = 0; t < NR; ++t) {
+              const int gi = soff[t] + (kst - st0) / p.group_steps;
+              const float sc = word_to_f32<SD>(sq[d][t], gi);
+              const float cz = HZ ? word_to_f32<SD>(zq[d][t], gi) - 128.f * sc : -136.f * sc;
+#pragma unroll
+              for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[t][mt][v] += sc * accg[t][mt][v] + cz * xsg[mt][v];
+                accg[t][mt] = z4;
+              }
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) xsg[mt] = z4;
+          }
+        }
+        request(d, kst + D - st0);
+      }
+    }
+  }
+  if (KIND == KIND_INT8) {
+#pragma unroll
+    for (int t = 0; t < NR; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[t][mt][v] -= 128.f * xsg[mt][v];
+  }
+
+  MIQ_TRACE(3);
+  // ---- epilogue: lane (r, g) holds y[16 mt + 4 g + v][nrow[t]]
+  const bool split = p.S > 1;
+#pragma unroll
+  for (int t = 0; t < NR; ++t) {
+    const int n = nrow[t];
+    if (n >= p.N) continue;
+    float rs = 1.f;
+    if (KIND == KIND_INT8 && !split) rs = bf16_to_f32(f32_to_bf16(sd_to_f32<SD>(load_sd_raw<SD>(p.scale, n))));
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = mt * 16 + g * 4 + v;
+        if (m >= M) continue;
+        const float o = acc[t][mt][v];
+        if (split) {
+          __hip_atomic_store(p.partial + ((int64_t)s * M + m) * p.N + n, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          p.y[(int64_t)m * p.ldy + n] = f32_to_bf16(KIND == KIND_INT8 ? bf16_to_f32(f32_to_bf16(o)) * rs : o);
+        }
+      }
+  }
+  if (!split) return;
+
+  // ---- split-K: the last workgroup of this row block adds the S partials in order
+  // this thread's partial stores have completed (the clobber keeps them above the wait)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  MIQ_TRACE(4);
+  __syncthreads();
+  __shared__ int s_last;
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(p.counters + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.S - 1;
+  __syncthreads();
+  if (!s_last) return;
+  constexpr int kRows = kWaves * NR * 16;
+  for (int i = tid; i < M * kRows; i += kThreads) {  // consecutive threads: consecutive n
+    const int m = i / kRows, n = nblk0 + (i - m * kRows);
+    if (n >= p.N) continue;
+    // the S partials are requested 8 at a time (independent loads, one round trip per 8
+    // splits) and added in split order
+    const float* src = p.partial + (int64_t)m * p.N + n;
+    const int64_t sstride = (int64_t)M * p.N;
+    float o = 0.f;
+    for (int s0 = 0; s0 < p.S; s0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        v[j] = __hip_atomic_load(src + min(s0 + j, p.S - 1) * sstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < p.S) o += v[j];
+    }
+    if (KIND == KIND_INT8)
+      o = bf16_to_f32(f32_to_bf16(o)) * bf16_to_f32(f32_to_bf16(sd_to_f32<SD>(load_sd_raw<SD>(p.scale, n))));
+    p.y[(int64_t)m * p.ldy + n] = f32_to_bf16(o);
+  }
+  if (tid == 0) __hip_atomic_store(p.counters + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ------------------------------------------------------------------ host-side planning
+struct StreamPlan {
+  int MT, NR, D, S, units, unit_steps, blocks, chunk_steps;
+  size_t lds_bytes, partial_bytes;
+};
+
+constexpr int kLdsBudget = 80 * 1024;  // two workgroups per CU
+
+StreamPlan plan_stream(int kind, int64_t M, int64_t N, int64_t K, int group_steps) {
+  StreamPlan pl{};
+  const int64_t steps = K / kStepK;
+  pl.unit_steps = kind == KIND_INT4 ? group_steps : 1;
+  pl.units = (int)(steps / pl.unit_steps);
+  pl.MT = (int)((M + 15) / 16);
+  pl.NR = pl.MT >= 3 ? 2 : 1;
+  int S = 0;
+  const char* env = getenv("MIQ_WO_PLAN");  // "NR,S" override for tuning
+  int e_nr = 0, e_s = 0;
+  if (env && sscanf(env, "%d,%d", &e_nr, &e_s) == 2 && (e_nr == 1 || e_nr == 2) && e_s >= 1) {
+    if ((pl.MT == 2 && e_nr == 2) || (pl.MT < 3 && e_nr == 1)) pl.NR = e_nr;  // D-step chunks must fit LDS
+    S = e_s;
+  }
+  pl.D = (kind == KIND_INT4 ? 8 : 4) / pl.NR;  // Cfg<>::D
+  const int64_t rows = kWaves * pl.NR * 16;
+  pl.blocks = (int)((N + rows - 1) / rows);
+  if (S == 0) {
+    // decode rows (MT = 1): about 2 workgroups per CU; more rows: fewer, longer splits,
+    // since every split adds M x rows partials that the last workgroup reads back
+    // (measured on MI355X over the Qwen3 projection shapes)
+    if (pl.MT == 1) S = (int)((512 + pl.blocks - 1) / pl.blocks);
+    else S = (int)((pl.MT == 2 ? 320 : 160) / pl.blocks);
+    if (S < 1) S = 1;
+  }
+  if (S > pl.units) S = pl.units;
+  if (pl.blocks > kMaxCounters) S = 1;
+  pl.S = S < 1 ? 1 : S;
+  // x chunk: the split's whole range when it fits the LDS budget, in multiples of D
+  const int64_t range = (int64_t)((pl.units + pl.S - 1) / pl.S) * pl.unit_steps;
+  auto lds_for = [&](int64_t cs) { return (size_t)(M * (cs * kStepK + 8) * 2 + cs * 16 * pl.MT * 4); };
+  int64_t cs = (range + pl.D - 1) / pl.D * pl.D;
+  while (cs > pl.D && lds_for(cs) > (size_t)kLdsBudget) cs -= pl.D;
+  pl.chunk_steps = (int)cs;
+  pl.lds_bytes = lds_for(cs);
+  pl.partial_bytes = pl.S > 1 ? (size_t)pl.S * M * N * 4 : 0;
+  return pl;
+}
+
+template <int KIND, bool HZ, int SD, int MT, int NR>
+void launch_stream(const StreamParams& p, dim3 grid, size_t lds, hipStream_t st) {
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wo_stream_kernel<KIND, HZ, SD, MT, NR>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBudget);
+    attr = true;
+  }
+  hipLaunchKernelGGL((wo_stream_kernel<KIND, HZ, SD, MT, NR>), grid, dim3(kThreads), lds, st, p);
+}
+
+template <int KIND, bool HZ, int SD>
+void launch_mt(const StreamParams& p, const StreamPlan& pl, dim3 grid, hipStream_t st) {
+  const size_t lds = pl.lds_bytes;
+  switch (pl.MT * 4 + pl.NR) {
+    case 5: launch_stream<KIND, HZ, SD, 1, 1>(p, grid, lds, st); break;
+    case 9: launch_stream<KIND, HZ, SD, 2, 1>(p, grid, lds, st); break;
+    case 10: launch_stream<KIND, HZ, SD, 2, 2>(p, grid, lds, st); break;
+    case 13: launch_stream<KIND, HZ, SD, 3, 1>(p, grid, lds, st); break;
+    case 14: launch_stream<KIND, HZ, SD, 3, 2>(p, grid, lds, st); break;
+    case 17: launch_stream<KIND, HZ, SD, 4, 1>(p, grid, lds, st); break;
+    default: launch_stream<KIND, HZ, SD, 4, 2>(p, grid, lds, st); break;
+  }
+}
+
+template <int KIND, bool HZ>
+void launch_sd(int sd, const StreamParams& p, const StreamPlan& pl, dim3 grid, hipStream_t st) {
+  if (sd == MIQ_BF16) launch_mt<KIND, HZ, MIQ_BF16>(p, pl, grid, st);
+  else if (sd == MIQ_F16) launch_mt<KIND, HZ, MIQ_F16>(p, pl, grid, st);
+  else launch_mt<KIND, HZ, MIQ_F32>(p, pl, grid, st);
+}
+
+}  // namespace
+
+// Workspace bytes for a weight-only GEMM: arrival counters, then [S][M][N] fp32 partials.
+// int4 plans depend on the group size, so the size covers every group that divides K.
+size_t wo_stream_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits) {
+  if (M < 1 || M > 64 || N < 1 || K < kStepK) return kCounterBytes;
+  const int steps = (int)(K / kStepK);
+  size_t most = 0;
+  for (int gs = 1; gs <= steps; ++gs) {
+    if (steps % gs) continue;
+    const StreamPlan pl = plan_stream(weight_bits == 4 ? KIND_INT4 : KIND_INT8, M, N, K, gs);
+    if (pl.partial_bytes > most) most = pl.partial_bytes;
+    if (weight_bits != 4) break;
+  }
+  return kCounterBytes + most;
+}
+
+int wo_stream_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, const void* scale,
+                     const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int M,
+                     int N, int K, void* workspace, size_t ws_bytes, hipStream_t st, const char* name) {
+  const StreamPlan pl = plan_stream(kind, M, N, K, group_steps);
+  MIQ_REQUIRE(pl.lds_bytes <= (size_t)kLdsBudget, "%s: no LDS plan for M=%d", name, M);
+  MIQ_REQUIRE(pl.S == 1 || (pl.blocks <= kMaxCounters && pl.partial_bytes < (1u << 31)),
+              "%s: N=%d too large for a split-K plan", name, N);
+  MIQ_REQUIRE((int64_t)N * ldw < 0x7fff0000LL, "%s: weights of %lld bytes exceed 2 GiB", name, (long long)N * ldw);
+  const size_t need = kCounterBytes + pl.partial_bytes;
+  MIQ_REQUIRE(pl.S == 1 || (workspace != nullptr && ws_bytes >= need),
+              "%s: workspace of %zu bytes needed (got %zu)", name, need, ws_bytes);
+  StreamParams p{};
+  p.x = x;
+  p.ldx = ldx;
+  p.w = w;
+  p.ldw = ldw;
+  p.scale = scale;
+  p.zero = zero;
+  p.group_steps = group_steps;
+  p.ngroups = ngroups;
+  p.y = y;
+  p.ldy = ldy;
+  p.M = M;
+  p.N = N;
+  p.S = pl.S;
+  p.units = pl.units;
+  p.unit_steps = pl.unit_steps;
+  p.chunk_steps = pl.chunk_steps;
+  p.wbytes = (int)((int64_t)N * ldw);
+  const int esz = sd == MIQ_F32 ? 4 : 2;
+  p.sbytes = kind == KIND_INT4 ? (int)(((int64_t)N * ngroups * esz + 3) & ~3LL) : 0;
+  p.counters = static_cast<int*>(workspace);
+  p.partial = workspace ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes) : nullptr;
+  const dim3 grid((unsigned)pl.blocks, (unsigned)pl.S);
+  if (kind == KIND_INT8) launch_sd<KIND_INT8, false>(sd, p, pl, grid, st);
+  else if (zero) launch_sd<KIND_INT4, true>(sd, p, pl, grid, st);
+  else launch_sd<KIND_INT4, false>(sd, p, pl, grid, st);
+  return check_launch(name);
+}
+
+}  // namespace miq

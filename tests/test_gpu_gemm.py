@@ -82,7 +82,9 @@ def test_w8a16_fp32_scale_and_strided_x():
 
 INT4_SHAPES = [(1, 64, 256, 128), (5, 128, 512, 128), (8, 64, 1024, 256), (16, 192, 384, 128),
                (33, 64, 512, 128), (64, 128, 768, 128), (1, 2560, 9728, 128), (8, 2560, 9728, 128),
-               (32, 2560, 9728, 128), (64, 2560, 9728, 128)]
+               (32, 2560, 9728, 128), (64, 2560, 9728, 128),
+               # large groups (a group spans several chunks / the whole split range), ragged N
+               (64, 256, 4096, 1024), (20, 144, 2048, 2048), (1, 512, 8192, 4096), (40, 80, 1024, 256)]
 
 
 @pytest.mark.parametrize("M,N,K,group", INT4_SHAPES)
@@ -100,6 +102,21 @@ def test_w4a16_gemm(M, N, K, group, symmetric):
     within(y, want)
     ref = O.int4_linear(x, **q)
     assert rel(ref, want) < 0.01 and rel(y, ref) < 0.01
+
+
+@pytest.mark.parametrize("sdt", [torch.float16, torch.float32])
+def test_w4a16_scale_dtypes(sdt):
+    """Scales / zeros stored as f16 or f32 (the kernels read them at storage precision)."""
+    from kernels import quant_ops as ops
+    case(f"w4a16 scale dtype {sdt}")
+    M, N, K, group = 8, 320, 2048, 256
+    w = make_w(N, K, 40)
+    x = make_x(M, K, 41)
+    q = O.int4_quantize(w, group)
+    q["scale"], q["zero"] = q["scale"].to(sdt), q["zero"].to(sdt)
+    want = O.int4_linear_fp32(x, **q)
+    y = ops.w4a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV), q["zero"].to(DEV))
+    within(y, want)
 
 
 def test_split_k_repeated_calls_are_identical():
