@@ -313,6 +313,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["headline", "all"], default="all")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a 256 MiB fill and a 256 MiB sum (the reference kernels for scaling "
+                         "rocprofv3 WRITE_SIZE / FETCH_SIZE readings to bytes)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the quantized path has no multi-GPU code (every GPU box "
@@ -330,6 +333,15 @@ def main():
     cfg, step_bytes, t = bench_headline(dev, args.steps, args.warmup)
     del cfg
     torch.cuda.empty_cache()
+    if args.copy_probe:
+        # known-size reference kernels: a 256 MiB fill (writes 256 MiB) and a sum over it
+        # (reads 256 MiB); the buffer is 256 MiB, the same as the MALL, so a second 256 MiB
+        # fill in between evicts it before the sum
+        a = torch.empty(64 * 2 ** 20, dtype=torch.float32, device=dev).fill_(1.0)
+        b = torch.empty_like(a).fill_(2.0)
+        a.sum()
+        torch.cuda.synchronize()
+        del a, b
     ms_per_step = t / args.steps * 1e3
     value = step_bytes * args.steps / t / 1e9
     avg_kernel_us = t / (4 * args.steps) * 1e6
@@ -367,7 +379,7 @@ def main():
                                "one step = M in {1,8,32,64}", "global_batch": list(MS), "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "wo_gemm_kernel<KIND_INT4>", "avg_kernel_us": round(avg_kernel_us, 3)},
+                     "kernel": "wo_stream_kernel<KIND_INT4>", "avg_kernel_us": round(avg_kernel_us, 3)},
         "cpu_baseline": cpu,
         "breakdown": breakdown,
     }
