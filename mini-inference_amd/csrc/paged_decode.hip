@@ -19,7 +19,13 @@
 // decodes of the stored codes. The wavefronts' softmax states are merged through LDS;
 // each workgroup writes its normalised partial output and log-sum-exp, and a second
 // kernel merges the partitions of each (request, head).
+#include <stdlib.h>
+
 #include "miq_common.h"
+
+#ifndef MIQ_TRACE
+#define MIQ_TRACE(point)
+#endif
 
 namespace miq {
 namespace {
@@ -47,6 +53,7 @@ struct AttnParams {
   int64_t bt_stride;
   const int32_t* lens;
   int H, KV, group, page;
+  int page_shift;  // log2(page) when page is a power of two, else -1
   float sm_scale;
   int partition, max_parts;
   float* o_part;
@@ -92,15 +99,29 @@ __device__ inline void wave_lds_sync() {
   __builtin_amdgcn_wave_barrier();
 }
 
-// max / sum over the 16 lanes that share lane / 16
+// max / sum over the 16 lanes that share lane / 16 (one DPP row), every lane getting
+// the result: swaps within quads (quad_perm 1,0,3,2 and 2,3,0,1), then rotations of the
+// row by 4 and 8. DPP moves are VALU operations; a lane shuffle would go through LDS.
+template <int CTRL>
+__device__ inline float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
 __device__ inline float max16(float v) {
-  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x124>(v));
+  return fmaxf(v, dpp_f<0x128>(v));
 }
 __device__ inline float sum16(float v) {
-  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x124>(v);
+  return v + dpp_f<0x128>(v);
 }
+
+// 2^x for x <= 0 (softmax weights): the hardware exponential, without the wrapper that
+// keeps results below 2^-126 normal (such weights are zero for this purpose)
+__device__ inline float exp2_le0(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <int KVT, bool HAS_SCALE, int SD>
 __global__ void __launch_bounds__(kWaves * 64)
@@ -194,9 +215,9 @@ paged_decode_split_kernel(AttnParams p) {
       const float mn = fmaxf(m_run[v], mt);
       // a head row that has seen no valid token keeps m = -inf; guard the exp2 arguments
       const float msafe = mn == -__builtin_inff() ? 0.f : mn;
-      alpha[v] = exp2f(m_run[v] - msafe);
+      alpha[v] = exp2_le0(m_run[v] - msafe);
       m_run[v] = mn;
-      const float e0 = exp2f(sc[0][v] - msafe), e1 = exp2f(sc[1][v] - msafe);
+      const float e0 = exp2_le0(sc[0][v] - msafe), e1 = exp2_le0(sc[1][v] - msafe);
       sc[0][v] = e0;
       sc[1][v] = e1;
       l_run[v] = l_run[v] * alpha[v] + e0 + e1;
@@ -317,6 +338,255 @@ paged_decode_split_kernel(AttnParams p) {
   }
 }
 
+// 8-bit caches (fp8 / int8): the same computation, organised for few instructions per
+// token and the memory traffic of a whole chunk of CS x 32 tokens per wavefront in
+// flight at once:
+//   * the slots of the chunk are looked up first (one round of block-table loads; a
+//     power-of-two page size turns the divisions into shifts), then every K, V and
+//     per-token scale load of the chunk is issued before any of them is used;
+//   * the scores of the whole chunk are computed first, so the running max, the rescale
+//     of the output accumulators and the DPP row reductions happen once per chunk
+//     rather than once per 32 tokens;
+//   * P goes to LDS through the hardware float -> bf16 conversion; V is dequantized,
+//     transposed in registers (byte permutes) and written to LDS per 32-token step;
+//     masking of V past the context is only done in the chunk that reaches it.
+template <int KVT, bool HAS_SCALE, int SD, int CS>
+__global__ void __launch_bounds__(kWaves * 64)
+paged_decode_split8_kernel(AttnParams p) {
+  const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int L = p.lens[b];
+  const int p0 = part * p.partition;
+  if (part > 0 && p0 >= L) return;  // partition beyond this request's context
+  MIQ_TRACE(0);
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int GROUP = p.group;
+  constexpr int kChunk = CS * kStep;
+
+  __shared__ __align__(16) uint16_t s_p[kWaves][16 * kPRow];
+  __shared__ __align__(16) uint16_t s_vt[kWaves][kD * kVRow];
+  __shared__ float s_m[kWaves][16], s_l[kWaves][16];
+
+  bf16x8 qf[4];
+  {
+    const bool real = r < GROUP;
+    const uint16_t* qp = p.q + (int64_t)b * p.qs_b + (int64_t)(kvh * GROUP + (real ? r : 0)) * p.qs_h + g * 32;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint4 u = real ? *reinterpret_cast<const uint4*>(qp + j * 8) : make_uint4(0, 0, 0, 0);
+      qf[j] = bf16x8_from(u.x, u.y, u.z, u.w);
+    }
+  }
+  for (int i = lane; i < 16 * kPRow; i += 64) s_p[wv][i] = 0;
+
+  const int per_wave = p.partition / kWaves;
+  const int t_begin = p0 + wv * per_wave;
+  const int t_end = min(t_begin + per_wave, L);
+  const float qk_scale = p.sm_scale * kLog2e;
+
+  float m_run[4], l_run[4];
+  f32x4 o_acc[8];
+#pragma unroll
+  for (int v = 0; v < 4; ++v) { m_run[v] = -__builtin_inff(); l_run[v] = 0.f; }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o_acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int64_t head_off = (int64_t)kvh * p.kvs_h;
+  const int32_t* btrow = p.bt + (int64_t)b * p.bt_stride;
+  uint16_t* vt = s_vt[wv];
+  uint16_t* pp = s_p[wv];
+  const int tq = (lane >> 3) * 4, dseg = (lane & 7) * 16;  // V: 4 tokens x 16 d per lane
+  const int pshift = p.page_shift, page = p.page;
+  auto slot_of = [&](int t) -> int64_t {
+    if (pshift >= 0) return ((int64_t)btrow[t >> pshift] << pshift) + (t & (page - 1));
+    return (int64_t)btrow[t / page] * page + t % page;
+  };
+
+  for (int c0 = t_begin; c0 < t_end; c0 += kChunk) {
+    // ---- slots: K / P tokens c0 + 32 s + 16 c + r, V tokens c0 + 32 s + tq + i
+    int64_t kslot[CS][2], vslot[CS][4];
+#pragma unroll
+    for (int s = 0; s < CS; ++s) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) kslot[s][c] = slot_of(min(c0 + s * kStep + c * 16 + r, t_end - 1));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vslot[s][i] = slot_of(min(c0 + s * kStep + tq + i, t_end - 1));
+    }
+    if (c0 == t_begin) MIQ_TRACE(1);
+    // ---- every K / V / scale load of the chunk
+    uint4 kr[CS][2][2], vr[CS][4];
+    uint32_t ksr[CS][2], vsr[CS][2];
+#pragma unroll
+    for (int s = 0; s < CS; ++s) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const uint8_t* kp = p.k + kslot[s][c] * p.kvs_t + head_off + g * 32;
+        kr[s][c][0] = *reinterpret_cast<const uint4*>(kp);
+        kr[s][c][1] = *reinterpret_cast<const uint4*>(kp + 16);
+        if (HAS_SCALE) {
+          const int64_t si = kslot[s][c] * p.ss_t + (int64_t)kvh * p.ss_h;
+          ksr[s][c] = load_sd_raw<SD>(p.ks, si);
+          vsr[s][c] = load_sd_raw<SD>(p.vs, si);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vr[s][i] = *reinterpret_cast<const uint4*>(p.v + vslot[s][i] * p.kvs_t + head_off + dseg);
+    }
+
+    // ---- scores of the chunk: lane holds heads 4 g + v of tokens c0 + 32 s + 16 c + r
+    float sc[CS][2][4];
+#pragma unroll
+    for (int s = 0; s < CS; ++s) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        bf16x8 kf[4];
+        uint32_t o[4];
+        bytes8_to_bf16<KVT>(kr[s][c][0].x, kr[s][c][0].y, o); kf[0] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        bytes8_to_bf16<KVT>(kr[s][c][0].z, kr[s][c][0].w, o); kf[1] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        bytes8_to_bf16<KVT>(kr[s][c][1].x, kr[s][c][1].y, o); kf[2] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        bytes8_to_bf16<KVT>(kr[s][c][1].z, kr[s][c][1].w, o); kf[3] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        f32x4 s4 = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s4 = mfma16(qf[j], kf[j], s4);
+        const bool valid = c0 + s * kStep + c * 16 + r < t_end;
+        const float kscale = HAS_SCALE ? qk_scale * sd_to_f32<SD>(ksr[s][c]) : qk_scale;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sc[s][c][v] = valid ? s4[v] * kscale : -__builtin_inff();
+      }
+    }
+    // ---- one online-softmax update for the whole chunk
+    float alpha[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float mt = sc[0][0][v];
+#pragma unroll
+      for (int s = 0; s < CS; ++s)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) mt = fmaxf(mt, sc[s][c][v]);
+      mt = max16(mt);
+      const float mn = fmaxf(m_run[v], mt);
+      const float msafe = mn == -__builtin_inff() ? 0.f : mn;  // a head with no valid token yet
+      alpha[v] = exp2_le0(m_run[v] - msafe);
+      m_run[v] = mn;
+      float lsum = 0.f;
+#pragma unroll
+      for (int s = 0; s < CS; ++s)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          sc[s][c][v] = exp2_le0(sc[s][c][v] - msafe);
+          lsum += sc[s][c][v];
+        }
+      l_run[v] = l_run[v] * alpha[v] + lsum;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) o_acc[j][v] *= alpha[v];
+    if (c0 == t_begin) MIQ_TRACE(2);
+
+    // ---- O += P V, 32 tokens at a time
+    const bool partial = c0 + kChunk > t_end;
+#pragma unroll
+    for (int s = 0; s < CS; ++s) {
+      const int t0 = c0 + s * kStep;
+      if (t0 < t_end) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const float vsc = HAS_SCALE ? sd_to_f32<SD>(vsr[s][c]) : 1.f;
+#pragma unroll
+          for (int v = 0; v < 4; ++v) {
+            const int h = g * 4 + v;
+            if (h < GROUP) pp[h * kPRow + c * 16 + r] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(sc[s][c][v] * vsc));
+          }
+        }
+        uint32_t vals[4][8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          uint32_t o[4];
+          bytes8_to_bf16<KVT>(vr[s][i].x, vr[s][i].y, o);
+          vals[i][0] = o[0]; vals[i][1] = o[1]; vals[i][2] = o[2]; vals[i][3] = o[3];
+          bytes8_to_bf16<KVT>(vr[s][i].z, vr[s][i].w, o);
+          vals[i][4] = o[0]; vals[i][5] = o[1]; vals[i][6] = o[2]; vals[i][7] = o[3];
+        }
+        if (partial) {  // zero V of masked tokens (P is 0 there, but 0 * NaN is NaN)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool dead = t0 + tq + i >= t_end;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vals[i][e] = dead ? 0u : vals[i][e];
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+#pragma unroll
+          for (int hfl = 0; hfl < 2; ++hfl) {
+            const uint32_t sel = hfl ? 0x07060302u : 0x05040100u;
+            const uint32_t a01 = __builtin_amdgcn_perm(vals[1][e], vals[0][e], sel);
+            const uint32_t a23 = __builtin_amdgcn_perm(vals[3][e], vals[2][e], sel);
+            const int d = dseg + e * 2 + hfl;
+            // 8-token groups are XOR-swizzled by (d / 16) % 4: without it the 8 lanes
+            // that share tq (rows 16 apart) hit the same LDS bank
+            const int col = (((tq >> 3) ^ ((d >> 4) & 3)) << 3) | (tq & 7);
+            *reinterpret_cast<uint2*>(vt + d * kVRow + col) = make_uint2(a01, a23);
+          }
+        }
+        wave_lds_sync();
+        {
+          const uint4 pa = *reinterpret_cast<const uint4*>(pp + r * kPRow + g * 8);
+          const bf16x8 pf = bf16x8_from(pa.x, pa.y, pa.z, pa.w);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const uint4 vb = *reinterpret_cast<const uint4*>(vt + (j * 16 + r) * kVRow + ((g ^ (j & 3)) << 3));
+            o_acc[j] = mfma16(pf, bf16x8_from(vb.x, vb.y, vb.z, vb.w), o_acc[j]);
+          }
+        }
+        wave_lds_sync();
+      }
+    }
+  }
+  MIQ_TRACE(3);
+
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const float lsum = sum16(l_run[v]);
+    if (r == 0) {
+      s_m[wv][g * 4 + v] = m_run[v];
+      s_l[wv][g * 4 + v] = lsum;
+    }
+  }
+  float* s_o_w = reinterpret_cast<float*>(s_vt[wv]);
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) s_o_w[(g * 4 + v) * (kD + 4) + j * 16 + r] = o_acc[j][v];
+  __syncthreads();
+
+  const int hh = tid >> 4, dq = (tid & 15) * 8;
+  if (hh < GROUP) {
+    float mx = -__builtin_inff();
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][hh]);
+    const float ms = mx == -__builtin_inff() ? 0.f : mx;
+    float lt = 0.f, sw[kWaves];
+    for (int w = 0; w < kWaves; ++w) {
+      sw[w] = exp2_le0(s_m[w][hh] - ms);
+      lt += s_l[w][hh] * sw[w];
+    }
+    const int h = kvh * GROUP + hh;
+    const int64_t base = ((int64_t)b * p.H + h) * p.max_parts + part;
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    float* op = p.o_part + base * kD + dq;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float o = 0.f;
+      for (int w = 0; w < kWaves; ++w)
+        o += reinterpret_cast<const float*>(s_vt[w])[hh * (kD + 4) + dq + e] * sw[w];
+      op[e] = o * inv;
+    }
+    if ((tid & 15) == 0) p.lse_part[base] = lt > 0.f ? (mx + log2f(lt)) * kLn2 : -__builtin_inff();
+  }
+  MIQ_TRACE(4);
+}
+
 // out[b, h] = sum_s exp(lse_s - max) o_s / sum_s exp(lse_s - max)
 __global__ void __launch_bounds__(kD)
 paged_decode_merge_kernel(const float* __restrict__ o_part, const float* __restrict__ lse_part,
@@ -343,7 +613,16 @@ paged_decode_merge_kernel(const float* __restrict__ o_part, const float* __restr
 
 template <int KVT, bool HS, int SD>
 void launch_split3(const AttnParams& p, dim3 grid, hipStream_t st) {
-  hipLaunchKernelGGL((paged_decode_split_kernel<KVT, HS, SD>), grid, dim3(kWaves * 64), 0, st, p);
+  if (KVT == MIQ_BF16) {
+    hipLaunchKernelGGL((paged_decode_split_kernel<KVT, HS, SD>), grid, dim3(kWaves * 64), 0, st, p);
+  } else {
+    static const int cs = [] {
+      const char* e = getenv("MIQ_ATTN_CHUNK");  // k-steps of 32 tokens per chunk, for tuning
+      return e && atoi(e) == 4 ? 4 : 2;
+    }();
+    if (cs == 2) hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2>), grid, dim3(kWaves * 64), 0, st, p);
+    else hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 4>), grid, dim3(kWaves * 64), 0, st, p);
+  }
 }
 
 template <int KVT, bool HS>
@@ -408,6 +687,7 @@ extern "C" int miq_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   p.KV = (int)KV;
   p.group = (int)(H / KV);
   p.page = (int)page;
+  p.page_shift = (page & (page - 1)) == 0 ? __builtin_ctzll((unsigned long long)page) : -1;
   p.sm_scale = sm_scale;
   p.partition = (int)partition;
   p.max_parts = (int)max_parts;
