@@ -126,7 +126,7 @@ __device__ inline float exp2_le0(float x) { return __builtin_amdgcn_exp2f(x); }
 template <int KVT, bool HAS_SCALE, int SD>
 __global__ void __launch_bounds__(kWaves * 64)
 paged_decode_split_kernel(AttnParams p) {
-  const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int part = blockIdx.y, kvh = blockIdx.x, b = blockIdx.z;  // kv heads of one partition are dispatched together (they share DRAM pages)
   const int L = p.lens[b];
   const int p0 = part * p.partition;
   if (part > 0 && p0 >= L) return;  // partition beyond this request's context
@@ -350,10 +350,10 @@ paged_decode_split_kernel(AttnParams p) {
 //   * P goes to LDS through the hardware float -> bf16 conversion; V is dequantized,
 //     transposed in registers (byte permutes) and written to LDS per 32-token step;
 //     masking of V past the context is only done in the chunk that reaches it.
-template <int KVT, bool HAS_SCALE, int SD, int CS>
-__global__ void __launch_bounds__(kWaves * 64)
+template <int KVT, bool HAS_SCALE, int SD, int CS, int NC, int W>
+__global__ void __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2)))
 paged_decode_split8_kernel(AttnParams p) {
-  const int part = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int part = blockIdx.y, kvh = blockIdx.x, b = blockIdx.z;  // kv heads of one partition are dispatched together (they share DRAM pages)
   const int L = p.lens[b];
   const int p0 = part * p.partition;
   if (part > 0 && p0 >= L) return;  // partition beyond this request's context
@@ -363,9 +363,14 @@ paged_decode_split8_kernel(AttnParams p) {
   const int GROUP = p.group;
   constexpr int kChunk = CS * kStep;
 
-  __shared__ __align__(16) uint16_t s_p[kWaves][16 * kPRow];
-  __shared__ __align__(16) uint16_t s_vt[kWaves][kD * kVRow];
-  __shared__ float s_m[kWaves][16], s_l[kWaves][16];
+  // per wavefront: P [16 heads][chunk tokens] bf16 and the chunk's V rows as stored
+  // (8-bit codes, row-major); after the token loop the V area holds the wave's O rows
+  constexpr int kPRowC = kChunk + 8;       // P row stride (bf16)
+  constexpr int kVRowB = kD + 16;          // V row stride (bytes)
+  constexpr int kVBytes = kChunk * kVRowB > 16 * (kD + 4) * 4 ? kChunk * kVRowB : 16 * (kD + 4) * 4;
+  __shared__ __align__(16) uint16_t s_p[W][16 * kPRowC];
+  __shared__ __align__(16) uint8_t s_v[W][kVBytes];
+  __shared__ float s_m[W][16], s_l[W][16];
 
   bf16x8 qf[4];
   {
@@ -377,9 +382,9 @@ paged_decode_split8_kernel(AttnParams p) {
       qf[j] = bf16x8_from(u.x, u.y, u.z, u.w);
     }
   }
-  for (int i = lane; i < 16 * kPRow; i += 64) s_p[wv][i] = 0;
+  for (int i = lane; i < 16 * kPRowC; i += 64) s_p[wv][i] = 0;
 
-  const int per_wave = p.partition / kWaves;
+  const int per_wave = p.partition / W;
   const int t_begin = p0 + wv * per_wave;
   const int t_end = min(t_begin + per_wave, L);
   const float qk_scale = p.sm_scale * kLog2e;
@@ -393,68 +398,91 @@ paged_decode_split8_kernel(AttnParams p) {
 
   const int64_t head_off = (int64_t)kvh * p.kvs_h;
   const int32_t* btrow = p.bt + (int64_t)b * p.bt_stride;
-  uint16_t* vt = s_vt[wv];
+  uint8_t* vl = s_v[wv];
   uint16_t* pp = s_p[wv];
   const int tq = (lane >> 3) * 4, dseg = (lane & 7) * 16;  // V: 4 tokens x 16 d per lane
   const int pshift = p.page_shift, page = p.page;
+  // NC > 0: the block-table entries of the partition are staged in LDS once per
+  // workgroup, so slot lookups are LDS reads instead of global loads that would queue
+  // behind (and so wait for) the K / V loads in flight
+  constexpr int kBtMax = NC > 0 ? W * NC * kChunk + 1 : 1;
+  __shared__ int s_bt[kBtMax];
+  const int pg0 = pshift >= 0 ? p0 >> pshift : p0 / page;
+  if (NC > 0) {
+    const int pg1 = (min(p0 + p.partition, L) - 1 + page) / page;  // one past the last page in use
+    for (int i = tid; i < pg1 - pg0; i += W * 64) s_bt[i] = btrow[pg0 + i];
+    __syncthreads();
+  }
   auto slot_of = [&](int t) -> int64_t {
+    if (NC > 0) {
+      if (pshift >= 0) return ((int64_t)s_bt[(t >> pshift) - pg0] << pshift) + (t & (page - 1));
+      return (int64_t)s_bt[t / page - pg0] * page + t % page;
+    }
     if (pshift >= 0) return ((int64_t)btrow[t >> pshift] << pshift) + (t & (page - 1));
     return (int64_t)btrow[t / page] * page + t % page;
   };
 
-  for (int c0 = t_begin; c0 < t_end; c0 += kChunk) {
-    // ---- slots: K / P tokens c0 + 32 s + 16 c + r, V tokens c0 + 32 s + tq + i
-    int64_t kslot[CS][2], vslot[CS][4];
+  // ---- the pieces of one chunk of CS x 32 tokens starting at c0
+  typedef int KSlots[CS][2];
+  typedef int VSlots[CS][4];
+  auto lookup = [&](int c0, KSlots& ks, VSlots& vs) {  // K / P tokens c0 + 32 s + 16 c + r, V tokens c0 + 32 s + tq + i
 #pragma unroll
     for (int s = 0; s < CS; ++s) {
 #pragma unroll
-      for (int c = 0; c < 2; ++c) kslot[s][c] = slot_of(min(c0 + s * kStep + c * 16 + r, t_end - 1));
+      for (int c = 0; c < 2; ++c) ks[s][c] = (int)slot_of(min(c0 + s * kStep + c * 16 + r, t_end - 1));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vslot[s][i] = slot_of(min(c0 + s * kStep + tq + i, t_end - 1));
+      for (int i = 0; i < 4; ++i) vs[s][i] = (int)slot_of(min(c0 + s * kStep + tq + i, t_end - 1));
     }
-    if (c0 == t_begin) MIQ_TRACE(1);
-    // ---- every K / V / scale load of the chunk
-    uint4 kr[CS][2][2], vr[CS][4];
-    uint32_t ksr[CS][2], vsr[CS][2];
+  };
+  constexpr int NB = NC > 1 ? 2 : 1;  // register sets (chunk c + 1 loads while chunk c computes)
+  uint4 kr[NB][CS][2][2], vr[NB][CS][4];
+  uint32_t ksr[NB][CS][2], vsr[NB][CS][2];
+  auto issue_k = [&](int bi, const KSlots& ks) {
 #pragma unroll
-    for (int s = 0; s < CS; ++s) {
+    for (int s = 0; s < CS; ++s)
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const uint8_t* kp = p.k + kslot[s][c] * p.kvs_t + head_off + g * 32;
-        kr[s][c][0] = *reinterpret_cast<const uint4*>(kp);
-        kr[s][c][1] = *reinterpret_cast<const uint4*>(kp + 16);
-        if (HAS_SCALE) {
-          const int64_t si = kslot[s][c] * p.ss_t + (int64_t)kvh * p.ss_h;
-          ksr[s][c] = load_sd_raw<SD>(p.ks, si);
-          vsr[s][c] = load_sd_raw<SD>(p.vs, si);
-        }
+        const uint8_t* kp = p.k + (int64_t)ks[s][c] * p.kvs_t + head_off + g * 32;
+        kr[bi][s][c][0] = *reinterpret_cast<const uint4*>(kp);
+        kr[bi][s][c][1] = *reinterpret_cast<const uint4*>(kp + 16);
+        if (HAS_SCALE) ksr[bi][s][c] = load_sd_raw<SD>(p.ks, (int64_t)ks[s][c] * p.ss_t + (int64_t)kvh * p.ss_h);
       }
+  };
+  // V rows, and the V scales of the K / P tokens (they scale P)
+  auto issue_v = [&](int bi, const KSlots& ks, const VSlots& vs) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vr[s][i] = *reinterpret_cast<const uint4*>(p.v + vslot[s][i] * p.kvs_t + head_off + dseg);
+    for (int s = 0; s < CS; ++s) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vr[bi][s][i] = *reinterpret_cast<const uint4*>(p.v + (int64_t)vs[s][i] * p.kvs_t + head_off + dseg);
+      if (HAS_SCALE) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) vsr[bi][s][c] = load_sd_raw<SD>(p.vs, (int64_t)ks[s][c] * p.ss_t + (int64_t)kvh * p.ss_h);
+      }
     }
-
-    // ---- scores of the chunk: lane holds heads 4 g + v of tokens c0 + 32 s + 16 c + r
-    float sc[CS][2][4];
+  };
+  float sc[CS][2][4];
+  // scores of the chunk (lane: heads 4 g + v of tokens c0 + 32 s + 16 c + r) and one
+  // online-softmax update for all of them
+  auto scores = [&](int bi, int c0) {
 #pragma unroll
     for (int s = 0; s < CS; ++s) {
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
         bf16x8 kf[4];
         uint32_t o[4];
-        bytes8_to_bf16<KVT>(kr[s][c][0].x, kr[s][c][0].y, o); kf[0] = bf16x8_from(o[0], o[1], o[2], o[3]);
-        bytes8_to_bf16<KVT>(kr[s][c][0].z, kr[s][c][0].w, o); kf[1] = bf16x8_from(o[0], o[1], o[2], o[3]);
-        bytes8_to_bf16<KVT>(kr[s][c][1].x, kr[s][c][1].y, o); kf[2] = bf16x8_from(o[0], o[1], o[2], o[3]);
-        bytes8_to_bf16<KVT>(kr[s][c][1].z, kr[s][c][1].w, o); kf[3] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        bytes8_to_bf16<KVT>(kr[bi][s][c][0].x, kr[bi][s][c][0].y, o); kf[0] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        bytes8_to_bf16<KVT>(kr[bi][s][c][0].z, kr[bi][s][c][0].w, o); kf[1] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        bytes8_to_bf16<KVT>(kr[bi][s][c][1].x, kr[bi][s][c][1].y, o); kf[2] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        bytes8_to_bf16<KVT>(kr[bi][s][c][1].z, kr[bi][s][c][1].w, o); kf[3] = bf16x8_from(o[0], o[1], o[2], o[3]);
         f32x4 s4 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 4; ++j) s4 = mfma16(qf[j], kf[j], s4);
         const bool valid = c0 + s * kStep + c * 16 + r < t_end;
-        const float kscale = HAS_SCALE ? qk_scale * sd_to_f32<SD>(ksr[s][c]) : qk_scale;
+        const float kscale = HAS_SCALE ? qk_scale * sd_to_f32<SD>(ksr[bi][s][c]) : qk_scale;
 #pragma unroll
         for (int v = 0; v < 4; ++v) sc[s][c][v] = valid ? s4[v] * kscale : -__builtin_inff();
       }
     }
-    // ---- one online-softmax update for the whole chunk
     float alpha[4];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -482,65 +510,96 @@ paged_decode_split8_kernel(AttnParams p) {
     for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int v = 0; v < 4; ++v) o_acc[j][v] *= alpha[v];
-    if (c0 == t_begin) MIQ_TRACE(2);
-
-    // ---- O += P V, 32 tokens at a time
+  };
+  // O += P V for the chunk. The V rows go to LDS as stored (8-bit, token-major) and come
+  // back through the transposing read ds_read_b64_tr_b8: in each group of 16 lanes,
+  // lane i receives byte i of the 8 rows formed by the 8-byte pieces that lanes 2k and
+  // 2k + 1 point at; pointing lanes 2k, 2k + 1 at the two halves of a 16-d block of
+  // token 8 g + k gives lane (g, i) the 8 tokens 8 g .. 8 g + 7 of column d = 16 j + i,
+  // which is the MFMA B operand.
+  auto pv = [&](int bi, int c0) {
     const bool partial = c0 + kChunk > t_end;
 #pragma unroll
     for (int s = 0; s < CS; ++s) {
-      const int t0 = c0 + s * kStep;
-      if (t0 < t_end) {
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-          const float vsc = HAS_SCALE ? sd_to_f32<SD>(vsr[s][c]) : 1.f;
+      for (int c = 0; c < 2; ++c) {
+        const float vsc = HAS_SCALE ? sd_to_f32<SD>(vsr[bi][s][c]) : 1.f;
 #pragma unroll
-          for (int v = 0; v < 4; ++v) {
-            const int h = g * 4 + v;
-            if (h < GROUP) pp[h * kPRow + c * 16 + r] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(sc[s][c][v] * vsc));
-          }
+        for (int v = 0; v < 4; ++v) {
+          const int h = g * 4 + v;
+          if (h < GROUP) pp[h * kPRowC + s * kStep + c * 16 + r] = __builtin_bit_cast(uint16_t, static_cast<__bf16>(sc[s][c][v] * vsc));
         }
-        uint32_t vals[4][8];
+      }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < 4; ++i) {
+        uint4 v = vr[bi][s][i];
+        if (partial && c0 + s * kStep + tq + i >= t_end) v = make_uint4(0, 0, 0, 0);  // 0 * NaN is NaN
+        *reinterpret_cast<uint4*>(vl + (s * kStep + tq + i) * kVRowB + dseg) = v;
+      }
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int s = 0; s < CS; ++s) {
+      if (c0 + s * kStep < t_end) {
+        const uint4 pa = *reinterpret_cast<const uint4*>(pp + r * kPRowC + s * kStep + g * 8);
+        const bf16x8 pf = bf16x8_from(pa.x, pa.y, pa.z, pa.w);
+        const uint8_t* vrow = vl + (s * kStep + 8 * g + (r >> 1)) * kVRowB + (r & 1) * 8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          typedef int v2i __attribute__((ext_vector_type(2)));
+          const v2i t8 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+              (__attribute__((address_space(3))) v2i*)(vrow + j * 16));
           uint32_t o[4];
-          bytes8_to_bf16<KVT>(vr[s][i].x, vr[s][i].y, o);
-          vals[i][0] = o[0]; vals[i][1] = o[1]; vals[i][2] = o[2]; vals[i][3] = o[3];
-          bytes8_to_bf16<KVT>(vr[s][i].z, vr[s][i].w, o);
-          vals[i][4] = o[0]; vals[i][5] = o[1]; vals[i][6] = o[2]; vals[i][7] = o[3];
+          bytes8_to_bf16<KVT>((uint32_t)t8[0], (uint32_t)t8[1], o);
+          o_acc[j] = mfma16(pf, bf16x8_from(o[0], o[1], o[2], o[3]), o_acc[j]);
         }
-        if (partial) {  // zero V of masked tokens (P is 0 there, but 0 * NaN is NaN)
+      }
+    }
+    wave_lds_sync();
+  };
+
+  if constexpr (NC == 0) {
+    // any partition: chunk after chunk
+    for (int c0 = t_begin; c0 < t_end; c0 += kChunk) {
+      KSlots ks;
+      VSlots vs;
+      lookup(c0, ks, vs);
+      issue_k(0, ks);
+      issue_v(0, ks, vs);
+      scores(0, c0);
+      pv(0, c0);
+    }
+  } else {
+    // the wave's NC chunks, unrolled as a pipeline over two register sets: the loads of
+    // chunk c + 1 are in flight while chunk c is computed, and chunk c + 2 is requested
+    // as soon as chunk c's registers are free
+    if (t_begin < t_end) {
+      KSlots ks;
+      VSlots vs;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const bool dead = t0 + tq + i >= t_end;
+      for (int c = 0; c < NB; ++c) {
+        const int c0 = t_begin + c * kChunk;
+        if (c == 0 || c0 < t_end) {
+          lookup(c0, ks, vs);
+          issue_k(c, ks);
+          issue_v(c, ks, vs);
+        }
+      }
+      MIQ_TRACE(1);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vals[i][e] = dead ? 0u : vals[i][e];
+      for (int c = 0; c < NC; ++c) {
+        const int c0 = t_begin + c * kChunk;
+        if (c0 < t_end) {
+          const int bi = c % NB;
+          scores(bi, c0);
+          if (c == 0) MIQ_TRACE(2);
+          pv(bi, c0);
+          if (c + NB < NC && c0 + NB * kChunk < t_end) {
+            lookup(c0 + NB * kChunk, ks, vs);
+            issue_k(bi, ks);
+            issue_v(bi, ks, vs);
           }
         }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-#pragma unroll
-          for (int hfl = 0; hfl < 2; ++hfl) {
-            const uint32_t sel = hfl ? 0x07060302u : 0x05040100u;
-            const uint32_t a01 = __builtin_amdgcn_perm(vals[1][e], vals[0][e], sel);
-            const uint32_t a23 = __builtin_amdgcn_perm(vals[3][e], vals[2][e], sel);
-            const int d = dseg + e * 2 + hfl;
-            // 8-token groups are XOR-swizzled by (d / 16) % 4: without it the 8 lanes
-            // that share tq (rows 16 apart) hit the same LDS bank
-            const int col = (((tq >> 3) ^ ((d >> 4) & 3)) << 3) | (tq & 7);
-            *reinterpret_cast<uint2*>(vt + d * kVRow + col) = make_uint2(a01, a23);
-          }
-        }
-        wave_lds_sync();
-        {
-          const uint4 pa = *reinterpret_cast<const uint4*>(pp + r * kPRow + g * 8);
-          const bf16x8 pf = bf16x8_from(pa.x, pa.y, pa.z, pa.w);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const uint4 vb = *reinterpret_cast<const uint4*>(vt + (j * 16 + r) * kVRow + ((g ^ (j & 3)) << 3));
-            o_acc[j] = mfma16(pf, bf16x8_from(vb.x, vb.y, vb.z, vb.w), o_acc[j]);
-          }
-        }
-        wave_lds_sync();
       }
     }
   }
@@ -554,20 +613,20 @@ paged_decode_split8_kernel(AttnParams p) {
       s_l[wv][g * 4 + v] = lsum;
     }
   }
-  float* s_o_w = reinterpret_cast<float*>(s_vt[wv]);
+  float* s_o_w = reinterpret_cast<float*>(s_v[wv]);
 #pragma unroll
   for (int j = 0; j < 8; ++j)
 #pragma unroll
     for (int v = 0; v < 4; ++v) s_o_w[(g * 4 + v) * (kD + 4) + j * 16 + r] = o_acc[j][v];
   __syncthreads();
 
-  const int hh = tid >> 4, dq = (tid & 15) * 8;
-  if (hh < GROUP) {
+  for (int e2 = tid; e2 < GROUP * 16; e2 += W * 64) {
+    const int hh = e2 >> 4, dq = (e2 & 15) * 8;
     float mx = -__builtin_inff();
-    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, s_m[w][hh]);
+    for (int w = 0; w < W; ++w) mx = fmaxf(mx, s_m[w][hh]);
     const float ms = mx == -__builtin_inff() ? 0.f : mx;
-    float lt = 0.f, sw[kWaves];
-    for (int w = 0; w < kWaves; ++w) {
+    float lt = 0.f, sw[W];
+    for (int w = 0; w < W; ++w) {
       sw[w] = exp2_le0(s_m[w][hh] - ms);
       lt += s_l[w][hh] * sw[w];
     }
@@ -578,11 +637,11 @@ paged_decode_split8_kernel(AttnParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float o = 0.f;
-      for (int w = 0; w < kWaves; ++w)
-        o += reinterpret_cast<const float*>(s_vt[w])[hh * (kD + 4) + dq + e] * sw[w];
+      for (int w = 0; w < W; ++w)
+        o += reinterpret_cast<const float*>(s_v[w])[hh * (kD + 4) + dq + e] * sw[w];
       op[e] = o * inv;
     }
-    if ((tid & 15) == 0) p.lse_part[base] = lt > 0.f ? (mx + log2f(lt)) * kLn2 : -__builtin_inff();
+    if ((e2 & 15) == 0) p.lse_part[base] = lt > 0.f ? (mx + log2f(lt)) * kLn2 : -__builtin_inff();
   }
   MIQ_TRACE(4);
 }
@@ -616,12 +675,12 @@ void launch_split3(const AttnParams& p, dim3 grid, hipStream_t st) {
   if (KVT == MIQ_BF16) {
     hipLaunchKernelGGL((paged_decode_split_kernel<KVT, HS, SD>), grid, dim3(kWaves * 64), 0, st, p);
   } else {
-    static const int cs = [] {
-      const char* e = getenv("MIQ_ATTN_CHUNK");  // k-steps of 32 tokens per chunk, for tuning
-      return e && atoi(e) == 4 ? 4 : 2;
-    }();
-    if (cs == 2) hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2>), grid, dim3(kWaves * 64), 0, st, p);
-    else hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 4>), grid, dim3(kWaves * 64), 0, st, p);
+    // 512-token partitions (the benchmark's): 2 wavefronts x 4 chunks of 64 tokens
+    // each, pipelined; any other partition: 4 wavefronts, chunk after chunk
+    if (p.partition == 512)
+      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 4, 2>), grid, dim3(2 * 64), 0, st, p);
+    else
+      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 0, 4>), grid, dim3(4 * 64), 0, st, p);
   }
 }
 
@@ -694,7 +753,7 @@ extern "C" int miq_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   p.o_part = o_part;
   p.lse_part = lse_part;
   hipStream_t st = (hipStream_t)stream;
-  const dim3 grid((unsigned)max_parts, (unsigned)KV, (unsigned)B);
+  const dim3 grid((unsigned)KV, (unsigned)max_parts, (unsigned)B);
   const bool hs = k_scale != nullptr;
   if (kv_dtype == MIQ_BF16) launch_split<MIQ_BF16, false>(p, grid, st);
   else if (kv_dtype == MIQ_FP8_E4M3) {
