@@ -11,6 +11,10 @@
 // The grouped GEMMs reuse the weight-only core (wo_core.h): a workgroup takes one
 // 16-row tile of one expert, gathers its activation rows into LDS, and its four
 // wavefronts stream 16 weight rows each.
+#include <stdlib.h>
+
+#include <algorithm>
+
 #include "wo_core.h"
 
 namespace miq {
@@ -225,6 +229,221 @@ moe_down_kernel(MoeParams p, int chunk_steps) {
   }
 }
 
+// ---------------------------------------------------------------- streaming expert GEMMs
+// The expert GEMMs as persistent workgroups: work item = (expert tile of 16 rows, block
+// of weight rows); a workgroup walks items blockIdx.x, + gridDim.x, ... until the tiles
+// in use (num_padded) run out, so the grid does not scale with the tiles that could
+// exist. Per item the 16 activation rows of the tile are gathered into LDS (with the
+// per-k-step sums the +128 code offset needs), and each wavefront streams two 16-row
+// weight tiles through a ring of D k-steps of buffer loads, as the dense weight-only
+// GEMM does.
+//   gate_up (GU): wavefront w of item block b owns I columns c0 = 64 b + 16 w .. + 15:
+//                 tile 0 = gate rows c0.., tile 1 = up rows I + c0..; silu(gate) * up
+//                 is formed in registers and written to hbuf
+//   down (DN):    wavefront w owns H rows 128 b + 32 w .. + 31 (two tiles); the product
+//                 times the routing weight goes to ypair[pair]
+enum { MOE_GU = 0, MOE_DN = 1 };
+constexpr int kMoeD = 8;       // ring depth (k-steps)
+constexpr int kMoeChunk = 16;  // k-steps of activations staged at once
+
+template <int MODE, bool HZ, int SD>
+__global__ void __launch_bounds__(256)
+moe_stream_kernel(MoeParams p, int blocks_per_tile) {
+  extern __shared__ __align__(16) uint16_t lds[];
+  __shared__ int s_src[kTile];
+  constexpr int NR = 2, NL = 1, D = kMoeD;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int K = MODE == MOE_GU ? p.H : p.I;
+  const int steps = K / kStepK;
+  const int64_t ldw = K / 2;
+  const int rows_per_expert = MODE == MOE_GU ? 2 * p.I : p.H;
+  const int64_t ngroups = steps / p.group_steps;
+  const uint16_t* xbase = MODE == MOE_GU ? p.hidden : p.hbuf;
+  const int ldx = K;
+  const int npad = *p.num_padded;
+  const int xstride = kMoeChunk * kStepK + 8;
+  float* xsum = reinterpret_cast<float*>(lds + kTile * xstride);
+  const int wbytes = (int)((int64_t)p.E * rows_per_expert * ldw);
+  constexpr int esz = SD == MIQ_F32 ? 4 : 2;
+  const int sbytes = (int)(((int64_t)p.E * rows_per_expert * ngroups * esz + 3) & ~3LL);
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(MODE == MOE_GU ? p.gu_q : p.dn_q), 0, wbytes, 0x00020000);
+  const void* sbase = MODE == MOE_GU ? p.gu_s : p.dn_s;
+  const void* zbase = MODE == MOE_GU ? p.gu_z : p.dn_z;
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(sbase), 0, sbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t zrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(HZ ? zbase : sbase), 0, sbytes, 0x00020000);
+  constexpr int kOut = 0x7ffffff0;
+  int nsteps_v = steps;
+  asm volatile("" : "+v"(nsteps_v));
+
+  for (int item = blockIdx.x;; item += gridDim.x) {
+    const int tile = item / blocks_per_tile, blk = item - tile * blocks_per_tile;
+    if (tile * kTile >= npad) break;
+    const int e = p.expert_ids[tile];
+    // weight rows of this wavefront's two tiles (within the whole [E * rows] matrix)
+    int row[NR];
+    if (MODE == MOE_GU) {
+      const int c0 = blk * 64 + wv * 16;
+      row[0] = e * rows_per_expert + c0 + r;
+      row[1] = e * rows_per_expert + p.I + c0 + r;
+    } else {
+      const int n0 = blk * 128 + wv * 32;
+      row[0] = e * rows_per_expert + n0 + r;
+      row[1] = e * rows_per_expert + n0 + 16 + r;
+    }
+    int woff[NR], soff[NR];
+#pragma unroll
+    for (int t = 0; t < NR; ++t) {
+      woff[t] = (int)(row[t] * ldw) + g * 16;
+      soff[t] = (int)(row[t] * ngroups);
+    }
+    uint4 wq[D][NR][NL];
+    uint32_t sq[D][NR], zq[D][NR];
+    auto request = [&](int d, int kl) {
+      const int keep = (kl - nsteps_v) >> 31;
+#pragma unroll
+      for (int t = 0; t < NR; ++t) {
+        const int off = ((woff[t] + kl * 64) & keep) | (kOut & ~keep);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2 /* nt */);
+        wq[d][t][0] = *reinterpret_cast<const uint4*>(&v);
+        const int gi = soff[t] + kl / p.group_steps;
+        const int so = ((gi * esz) & ~3 & keep) | (kOut & ~keep);
+        sq[d][t] = __builtin_amdgcn_raw_buffer_load_b32(srs, so, 0, 0);
+        zq[d][t] = HZ ? __builtin_amdgcn_raw_buffer_load_b32(zrs, so, 0, 0) : 0u;
+      }
+    };
+    if (tid < kTile) {
+      const int pair = p.sorted_ids[tile * kTile + tid];
+      s_src[tid] = pair < p.num_pairs ? (MODE == MOE_GU ? pair / p.topk : tile * kTile + tid) : -1;
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) request(d, d);
+    __syncthreads();  // s_src ready (and the previous item is done with LDS)
+
+    f32x4 acc[NR], accg[NR], xsg;
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < NR; ++t) { acc[t] = z4; accg[t] = z4; }
+    xsg = z4;
+
+    for (int c0 = 0; c0 < steps; c0 += kMoeChunk) {
+      const int nst = min(kMoeChunk, steps - c0);
+      const int xcols = nst * (kStepK / 8);
+      const int npieces = kTile * xcols;
+      if (c0) __syncthreads();
+      for (int base = 0; base < npieces; base += 4 * 256) {
+        uint4 xr[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = min(base + tid + j * 256, npieces - 1);
+          const int m = i / xcols, c = i - m * xcols;
+          const int src = s_src[m];
+          xr[j] = src >= 0 ? *reinterpret_cast<const uint4*>(xbase + (int64_t)src * ldx + (int64_t)c0 * kStepK + c * 8)
+                           : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = base + tid + j * 256;
+          const int ic = min(i, npieces - 1);
+          const int m = ic / xcols, c = ic - m * xcols;
+          *reinterpret_cast<uint4*>(lds + m * xstride + c * 8) = permute_for_u4(xr[j]);
+          float sm = sum8_bf16(xr[j]);
+          sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x111, 0xf, 0xf, true));
+          sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x112, 0xf, 0xf, true));
+          sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x114, 0xf, 0xf, true));
+          sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x118, 0xf, 0xf, true));
+          if (i < npieces && (c & 15) == 15) xsum[(c >> 4) * kTile + m] = sm;
+        }
+      }
+      __syncthreads();
+      for (int k = c0; k < c0 + nst; k += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+          const int kst = k + d, kl = kst - c0;
+          if (kst < c0 + nst) {
+            const uint16_t* arow = lds + r * xstride;
+            bf16x8 av[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const uint4 v = *reinterpret_cast<const uint4*>(arow + a_off<KIND_INT4>(kl, g, j));
+              av[j] = as_bf16x8(v.x, v.y, v.z, v.w);
+            }
+            xsg += *reinterpret_cast<const f32x4*>(xsum + kl * kTile + g * 4);
+#pragma unroll
+            for (int t = 0; t < NR; ++t) {
+              bf16x8 bv[4];
+              unpack_b<KIND_INT4>(wq[d][t], bv);
+#pragma unroll
+              for (int j = 0; j < 4; ++j) accg[t] = mfma(av[j], bv[j], accg[t]);
+            }
+            if ((kst + 1) % p.group_steps == 0) {
+#pragma unroll
+              for (int t = 0; t < NR; ++t) {
+                const int gi = soff[t] + kst / p.group_steps;
+                const float sc = word_to_f32<SD>(sq[d][t], gi);
+                const float cz = HZ ? word_to_f32<SD>(zq[d][t], gi) - 128.f * sc : -136.f * sc;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[t][v] += sc * accg[t][v] + cz * xsg[v];
+                accg[t] = z4;
+              }
+              xsg = z4;
+            }
+          }
+          request(d, kst + D);
+        }
+      }
+    }
+
+    // epilogue: lane (r, g) holds rows m = 4 g + v of columns r of both tiles
+    if (MODE == MOE_GU) {
+      const int col = blk * 64 + wv * 16 + r;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = g * 4 + v;
+        const float gt = bf16r(acc[0][v]);
+        const float up = bf16r(acc[1][v]);
+        const float act = bf16r(gt / (1.f + __expf(-gt)));
+        p.hbuf[(int64_t)(tile * kTile + m) * p.I + col] = f32_to_bf16(act * up);
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = g * 4 + v;
+        const int pair = p.sorted_ids[tile * kTile + m];
+        if (pair < p.num_pairs) {
+          const float w = bf16_to_f32(p.topk_w[pair]);
+          const int n0 = blk * 128 + wv * 32 + r;
+          p.ypair[(int64_t)pair * p.H + n0] = bf16r(bf16r(acc[0][v]) * w);
+          p.ypair[(int64_t)pair * p.H + n0 + 16] = bf16r(bf16r(acc[1][v]) * w);
+        }
+      }
+    }
+  }
+}
+
+template <bool HZ, int SD>
+void launch_stream_experts(const MoeParams& p, int max_tiles, hipStream_t st) {
+  const int steps_gu = p.H / kStepK, steps_dn = p.I / kStepK;
+  const size_t lds_gu = (size_t)kTile * (kMoeChunk * kStepK + 8) * 2 + (size_t)kMoeChunk * kTile * 4;
+  const int bgu = p.I / 64, bdn = p.H / 128;
+  (void)steps_gu;
+  (void)steps_dn;
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_stream_kernel<MOE_GU, HZ, SD>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_gu);
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_stream_kernel<MOE_DN, HZ, SD>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_gu);
+    attr = true;
+  }
+  // about two workgroups per CU, never more than the items that could exist
+  const int grid_gu = std::min(512, max_tiles * bgu), grid_dn = std::min(512, max_tiles * bdn);
+  hipLaunchKernelGGL((moe_stream_kernel<MOE_GU, HZ, SD>), dim3(grid_gu), dim3(256), lds_gu, st, p, bgu);
+  hipLaunchKernelGGL((moe_stream_kernel<MOE_DN, HZ, SD>), dim3(grid_dn), dim3(256), lds_gu, st, p, bdn);
+}
+
 // out[t][n] = sum over slots j (in order) of ypair[t * k + j][n]
 __global__ void moe_combine_kernel(const float* __restrict__ ypair, int topk, int H, uint16_t* __restrict__ out) {
   const int t = blockIdx.y;
@@ -238,6 +457,10 @@ __global__ void moe_combine_kernel(const float* __restrict__ ypair, int topk, in
 template <bool HZ, int SD>
 void launch_experts_t(const MoeParams& p, dim3 gu_grid, dim3 dn_grid, int gu_chunk, int dn_chunk, size_t gu_lds,
                       size_t dn_lds, hipStream_t st) {
+  if (p.H % 128 == 0 && p.I % 64 == 0 && !getenv("MIQ_MOE_TILED")) {
+    launch_stream_experts<HZ, SD>(p, (int)gu_grid.y, st);
+    return;
+  }
   hipLaunchKernelGGL((moe_gate_up_kernel<HZ, SD>), gu_grid, dim3(256), gu_lds, st, p, gu_chunk);
   hipLaunchKernelGGL((moe_down_kernel<HZ, SD>), dn_grid, dim3(256), dn_lds, st, p, dn_chunk);
 }
@@ -300,6 +523,8 @@ extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I
   MIQ_REQUIRE(((reinterpret_cast<uintptr_t>(hidden) | reinterpret_cast<uintptr_t>(gu_q) |
                 reinterpret_cast<uintptr_t>(dn_q)) & 15) == 0,
               "w4a16_moe: hidden and weights must be 16-byte aligned");
+  MIQ_REQUIRE(E * 2 * I * (H / 2) < 0x7fff0000LL && E * H * (I / 2) < 0x7fff0000LL,
+              "w4a16_moe: expert weights above 2 GiB");
   const size_t need = miq_moe_workspace_bytes(T, topk, E, H, I);
   MIQ_REQUIRE(workspace != nullptr && workspace_bytes >= need, "w4a16_moe: workspace of %zu bytes needed", need);
   MoeParams p{};

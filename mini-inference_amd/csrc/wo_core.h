@@ -117,6 +117,28 @@ __device__ inline void unpack_b(const uint4* w, bf16x8 b[4]) {
 }
 
 
+__device__ inline float sum8_bf16(uint4 v) {
+  const float lo = bf16_to_f32(v.x & 0xffff) + bf16_to_f32(v.y & 0xffff) + bf16_to_f32(v.z & 0xffff) +
+                   bf16_to_f32(v.w & 0xffff);
+  const float hi = bf16_to_f32(v.x >> 16) + bf16_to_f32(v.y >> 16) + bf16_to_f32(v.z >> 16) + bf16_to_f32(v.w >> 16);
+  return lo + hi;
+}
+
+// The aligned 32-bit word holding element i of a bf16 / f16 / f32 array (a 16-bit load
+// would be widened right where it is issued, which makes the compiler wait for it), and
+// the element's value from that word.
+template <int SD>
+__device__ inline uint32_t load_sd_word(const void* p, int64_t i) {
+  if constexpr (SD == MIQ_F32) return static_cast<const uint32_t*>(p)[i];
+  else return static_cast<const uint32_t*>(p)[i >> 1];
+}
+
+template <int SD>
+__device__ inline float word_to_f32(uint32_t w, int64_t i) {
+  if constexpr (SD == MIQ_F32) return __builtin_bit_cast(float, w);
+  else return sd_to_f32<SD>((i & 1) ? (w >> 16) : (w & 0xffffu));
+}
+
 // int4 group scales / zeros of the workgroup's rows, staged in LDS as raw bits:
 // sc[row * stride + (group - g0)], row = 16 t + r (NT tiles), groups g0 .. g0 + stride - 1.
 template <int SD>

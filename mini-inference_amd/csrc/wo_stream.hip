@@ -37,13 +37,20 @@
 #define MIQ_TRACE(point)
 #endif
 
+// ring depth (k-steps of int4 weights in flight per wavefront) for one activation tile;
+// 8 and 16 measured the same or 8 slightly better on the decode shapes
+#ifndef MIQ_D1
+#define MIQ_D1 8
+#endif
+
 namespace miq {
 namespace {
 
 using namespace wo;
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
+// wavefronts per workgroup (8 and 16 for decode tiles measured slower than 4)
+template <int MT>
+constexpr int waves_for() { return 4; }
 constexpr int kMaxCounters = 4096;   // row blocks that may use split-K
 constexpr int kCounterBytes = kMaxCounters * 4;
 
@@ -52,7 +59,7 @@ constexpr int kCounterBytes = kMaxCounters * 4;
 template <int KIND, int MT, int NR>
 struct Cfg {
   static constexpr int NL = KIND == KIND_INT4 ? 1 : 2;       // 16-byte loads per tile-step
-  static constexpr int D = (KIND == KIND_INT4 ? 8 : 4) / NR;  // ring depth in k-steps
+  static constexpr int D = (KIND == KIND_INT4 ? (MT == 1 ? MIQ_D1 : 8) : (MT == 1 ? MIQ_D1 / 2 : 4)) / NR;  // ring depth in k-steps
   static constexpr int XR = 16 * MT;                          // x-sum row pitch
   static constexpr int XP = 4;                                // staging pieces per thread per round
 };
@@ -76,31 +83,10 @@ struct StreamParams {
   int* counters;        // [kMaxCounters]
 };
 
-__device__ inline float sum8_bf16(uint4 v) {
-  const float lo = bf16_to_f32(v.x & 0xffff) + bf16_to_f32(v.y & 0xffff) + bf16_to_f32(v.z & 0xffff) +
-                   bf16_to_f32(v.w & 0xffff);
-  const float hi = bf16_to_f32(v.x >> 16) + bf16_to_f32(v.y >> 16) + bf16_to_f32(v.z >> 16) + bf16_to_f32(v.w >> 16);
-  return lo + hi;
-}
-
-// The aligned 32-bit word holding element i of a bf16 / f16 / f32 array (a 16-bit load
-// would be widened right where it is issued, which makes the compiler wait for it), and
-// the element's value from that word.
-template <int SD>
-__device__ inline uint32_t load_sd_word(const void* p, int64_t i) {
-  if constexpr (SD == MIQ_F32) return static_cast<const uint32_t*>(p)[i];
-  else return static_cast<const uint32_t*>(p)[i >> 1];
-}
-
-template <int SD>
-__device__ inline float word_to_f32(uint32_t w, int64_t i) {
-  if constexpr (SD == MIQ_F32) return __builtin_bit_cast(float, w);
-  else return sd_to_f32<SD>((i & 1) ? (w >> 16) : (w & 0xffffu));
-}
-
 template <int KIND, bool HZ, int SD, int MT, int NR>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(waves_for<MT>() * 64)
 wo_stream_kernel(StreamParams p) {
+  constexpr int kWaves = waves_for<MT>(), kThreads = kWaves * 64;
   using C = Cfg<KIND, MT, NR>;
   constexpr int D = C::D, NL = C::NL, XR = C::XR, XP = C::XP;
   constexpr int kStepBytes = KIND == KIND_INT4 ? kStepK / 2 : kStepK;  // per weight row
@@ -309,6 +295,7 @@ wo_stream_kernel(StreamParams p) {
   if (tid == 0)
     s_last = __hip_atomic_fetch_add(p.counters + blockIdx.x, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.S - 1;
   __syncthreads();
+  MIQ_TRACE(6);
   if (!s_last) return;
   constexpr int kRows = kWaves * NR * 16;
   for (int i = tid; i < M * kRows; i += kThreads) {  // consecutive threads: consecutive n
@@ -333,6 +320,7 @@ wo_stream_kernel(StreamParams p) {
     p.y[(int64_t)m * p.ldy + n] = f32_to_bf16(o);
   }
   if (tid == 0) __hip_atomic_store(p.counters + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  MIQ_TRACE(7);
 }
 
 // ------------------------------------------------------------------ host-side planning
@@ -357,8 +345,8 @@ StreamPlan plan_stream(int kind, int64_t M, int64_t N, int64_t K, int group_step
     if ((pl.MT == 2 && e_nr == 2) || (pl.MT < 3 && e_nr == 1)) pl.NR = e_nr;  // D-step chunks must fit LDS
     S = e_s;
   }
-  pl.D = (kind == KIND_INT4 ? 8 : 4) / pl.NR;  // Cfg<>::D
-  const int64_t rows = kWaves * pl.NR * 16;
+  pl.D = (kind == KIND_INT4 ? (pl.MT == 1 ? MIQ_D1 : 8) : (pl.MT == 1 ? MIQ_D1 / 2 : 4)) / pl.NR;  // Cfg<>::D
+  const int64_t rows = (pl.MT == 1 ? waves_for<1>() : waves_for<2>()) * pl.NR * 16;
   pl.blocks = (int)((N + rows - 1) / rows);
   if (S == 0) {
     // decode rows (MT = 1): about 2 workgroups per CU; more rows: fewer, longer splits,
@@ -390,7 +378,7 @@ void launch_stream(const StreamParams& p, dim3 grid, size_t lds, hipStream_t st)
                               hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBudget);
     attr = true;
   }
-  hipLaunchKernelGGL((wo_stream_kernel<KIND, HZ, SD, MT, NR>), grid, dim3(kThreads), lds, st, p);
+  hipLaunchKernelGGL((wo_stream_kernel<KIND, HZ, SD, MT, NR>), grid, dim3(waves_for<MT>() * 64), lds, st, p);
 }
 
 template <int KIND, bool HZ, int SD>
