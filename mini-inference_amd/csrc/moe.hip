@@ -31,26 +31,39 @@ __device__ inline int load_id(const void* ids, int dtype, int i) {
 __global__ void __launch_bounds__(1024)
 moe_align_kernel(const void* __restrict__ ids, int dtype, int num_pairs, int E, int bm, int max_padded,
                  int max_blocks, int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
-                 int32_t* __restrict__ num_padded) {
+                 int32_t* __restrict__ num_padded, int ids_in_lds) {
   extern __shared__ int sm[];
   int* counts = sm;               // [E]
   int* offsets = sm + E;          // [E + 1]
+  int* lid = sm + 2 * E + 1;      // [num_pairs] the expert ids, read from memory once (when they fit)
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), nw = blockDim.x >> 6;
+  auto id_at = [&](int i) { return ids_in_lds ? lid[i] : load_id(ids, dtype, i); };
   for (int e = tid; e < E; e += blockDim.x) counts[e] = 0;
+  if (ids_in_lds)
+    for (int i = tid; i < num_pairs; i += blockDim.x) lid[i] = load_id(ids, dtype, i);
   __syncthreads();
   for (int i = tid; i < num_pairs; i += blockDim.x) {
-    const int e = load_id(ids, dtype, i);
+    const int e = id_at(i);
     if (e >= 0 && e < E) atomicAdd(&counts[e], 1);
   }
   __syncthreads();
-  if (tid == 0) {
-    int total = 0;
-    offsets[0] = 0;
-    for (int e = 0; e < E; ++e) {
-      total += (counts[e] + bm - 1) / bm * bm;
-      offsets[e + 1] = total;
+  if (wv == 0) {  // exclusive scan of the padded counts, 64 experts per round
+    int carry = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      const int c = e < E ? (counts[e] + bm - 1) / bm * bm : 0;
+      int incl = c;
+      for (int o = 1; o < 64; o <<= 1) {
+        const int up = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += up;
+      }
+      if (e < E) offsets[e] = carry + incl - c;
+      carry += __shfl(incl, 63, 64);
     }
-    *num_padded = total;
+    if (lane == 0) {
+      offsets[E] = carry;
+      *num_padded = carry;
+    }
   }
   __syncthreads();
   for (int i = tid; i < max_padded; i += blockDim.x) sorted_ids[i] = num_pairs;
@@ -68,13 +81,14 @@ moe_align_kernel(const void* __restrict__ ids, int dtype, int num_pairs, int E, 
     }
     expert_ids[t] = owner;
   }
-  __syncthreads();
+  __syncthreads();  // the sentinel fill lands before the pairs are placed
+  // the pairs of expert e in ascending pair order: one wavefront per expert, ballots
   const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int e = wv; e < E; e += nw) {
     int base = offsets[e];
     for (int c0 = 0; c0 < num_pairs; c0 += 64) {
       const int i = c0 + lane;
-      const bool hit = i < num_pairs && load_id(ids, dtype, i) == e;
+      const bool hit = i < num_pairs && id_at(i) == e;
       const uint64_t mask = __ballot(hit);
       if (hit) sorted_ids[base + __popcll(mask & below)] = i;
       base += __popcll(mask);
@@ -243,7 +257,7 @@ moe_down_kernel(MoeParams p, int chunk_steps) {
 //   down (DN):    wavefront w owns H rows 128 b + 32 w .. + 31 (two tiles); the product
 //                 times the routing weight goes to ypair[pair]
 enum { MOE_GU = 0, MOE_DN = 1 };
-constexpr int kMoeD = 8;       // ring depth (k-steps)
+constexpr int kMoeD = 8;       // ring depth (k-steps; 16 measured slower)
 constexpr int kMoeChunk = 16;  // k-steps of activations staged at once
 
 template <int MODE, bool HZ, int SD>
@@ -496,9 +510,10 @@ extern "C" int miq_moe_align(const void* topk_ids, int idx_dtype, int64_t num_pa
               (long long)block_m);
   const int64_t max_padded = num_pairs + E * (block_m - 1);
   const int64_t max_blocks = (max_padded + block_m - 1) / block_m;
-  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(1024), (size_t)(2 * E + 1) * sizeof(int),
+  const int in_lds = (2 * E + 1 + num_pairs) * 4 <= 64 * 1024;
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(1024), (size_t)(2 * E + 1 + (in_lds ? num_pairs : 0)) * sizeof(int),
                      (hipStream_t)stream, topk_ids, idx_dtype, (int)num_pairs, (int)E, (int)block_m,
-                     (int)max_padded, (int)max_blocks, sorted_ids, expert_ids, num_padded);
+                     (int)max_padded, (int)max_blocks, sorted_ids, expert_ids, num_padded, in_lds);
   return check_launch("moe_align");
 }
 
