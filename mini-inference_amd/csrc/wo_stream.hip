@@ -297,27 +297,60 @@ wo_stream_kernel(StreamParams p) {
   __syncthreads();
   MIQ_TRACE(6);
   if (!s_last) return;
+  // 4 consecutive n per thread and round; the S partials of 4 such vectors are requested
+  // 4 splits at a time with agent-coherent (sc1) 16-byte loads, then added in split order
   constexpr int kRows = kWaves * NR * 16;
-  for (int i = tid; i < M * kRows; i += kThreads) {  // consecutive threads: consecutive n
-    const int m = i / kRows, n = nblk0 + (i - m * kRows);
-    if (n >= p.N) continue;
-    // the S partials are requested 8 at a time (independent loads, one round trip per 8
-    // splits) and added in split order
-    const float* src = p.partial + (int64_t)m * p.N + n;
-    const int64_t sstride = (int64_t)M * p.N;
-    float o = 0.f;
-    for (int s0 = 0; s0 < p.S; s0 += 8) {
-      float v[8];
+  constexpr int VB = 4;
+  const __amdgpu_buffer_rsrc_t prs =
+      __builtin_amdgcn_make_buffer_rsrc(p.partial, 0, (int)((int64_t)p.S * M * p.N * 4), 0x00020000);
+  const int nvec = M * (kRows / 4);
+  for (int v0 = tid; v0 < nvec; v0 += kThreads * VB) {
+    float4 o[VB];
+    int off[VB];
+    bool ok[VB];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        v[j] = __hip_atomic_load(src + min(s0 + j, p.S - 1) * sstride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (s0 + j < p.S) o += v[j];
+    for (int j = 0; j < VB; ++j) {
+      const int v = min(v0 + j * kThreads, nvec - 1);
+      const int m = v / (kRows / 4), n = nblk0 + (v - m * (kRows / 4)) * 4;
+      ok[j] = v0 + j * kThreads < nvec && n < p.N;
+      off[j] = (m * p.N + min(n, p.N - 4)) * 4;
+      o[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    if (KIND == KIND_INT8)
-      o = bf16_to_f32(f32_to_bf16(o)) * bf16_to_f32(f32_to_bf16(sd_to_f32<SD>(load_sd_raw<SD>(p.scale, n))));
-    p.y[(int64_t)m * p.ldy + n] = f32_to_bf16(o);
+    const int sstride = M * p.N * 4;
+    for (int s0 = 0; s0 < p.S; s0 += 4) {
+      float4 t[4][VB];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int j = 0; j < VB; ++j) {
+          const auto w = __builtin_amdgcn_raw_buffer_load_b128(prs, off[j] + min(s0 + u, p.S - 1) * sstride, 0, 16 /* sc1 */);
+          t[u][j] = *reinterpret_cast<const float4*>(&w);
+        }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (s0 + u < p.S)
+#pragma unroll
+          for (int j = 0; j < VB; ++j) {
+            o[j].x += t[u][j].x;
+            o[j].y += t[u][j].y;
+            o[j].z += t[u][j].z;
+            o[j].w += t[u][j].w;
+          }
+    }
+#pragma unroll
+    for (int j = 0; j < VB; ++j) {
+      if (!ok[j]) continue;
+      const int v = v0 + j * kThreads;
+      const int m = v / (kRows / 4), n = nblk0 + (v - m * (kRows / 4)) * 4;
+      const float f[4] = {o[j].x, o[j].y, o[j].z, o[j].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float val = f[e];
+        if (KIND == KIND_INT8)
+          val = bf16_to_f32(f32_to_bf16(val)) * bf16_to_f32(f32_to_bf16(sd_to_f32<SD>(load_sd_raw<SD>(p.scale, n + e))));
+        p.y[(int64_t)m * p.ldy + n + e] = f32_to_bf16(val);
+      }
+    }
   }
   if (tid == 0) __hip_atomic_store(p.counters + blockIdx.x, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   MIQ_TRACE(7);
@@ -337,7 +370,7 @@ StreamPlan plan_stream(int kind, int64_t M, int64_t N, int64_t K, int group_step
   pl.unit_steps = kind == KIND_INT4 ? group_steps : 1;
   pl.units = (int)(steps / pl.unit_steps);
   pl.MT = (int)((M + 15) / 16);
-  pl.NR = pl.MT >= 3 ? 2 : 1;
+  pl.NR = pl.MT >= 2 ? 2 : 1;
   int S = 0;
   const char* env = getenv("MIQ_WO_PLAN");  // "NR,S" override for tuning
   int e_nr = 0, e_s = 0;
@@ -349,11 +382,10 @@ StreamPlan plan_stream(int kind, int64_t M, int64_t N, int64_t K, int group_step
   const int64_t rows = (pl.MT == 1 ? waves_for<1>() : waves_for<2>()) * pl.NR * 16;
   pl.blocks = (int)((N + rows - 1) / rows);
   if (S == 0) {
-    // decode rows (MT = 1): about 2 workgroups per CU; more rows: fewer, longer splits,
-    // since every split adds M x rows partials that the last workgroup reads back
-    // (measured on MI355X over the Qwen3 projection shapes)
+    // about 2 workgroups per CU for one tile of activation rows, about 1.5 for more
+    // rows (measured on MI355X over the Qwen3 projection shapes)
     if (pl.MT == 1) S = (int)((512 + pl.blocks - 1) / pl.blocks);
-    else S = (int)((pl.MT == 2 ? 320 : 160) / pl.blocks);
+    else S = (int)((400 + pl.blocks / 2) / pl.blocks);
     if (S < 1) S = 1;
   }
   if (S > pl.units) S = pl.units;
