@@ -59,7 +59,10 @@ constexpr int kCounterBytes = kMaxCounters * 4;
 template <int KIND, int MT, int NR>
 struct Cfg {
   static constexpr int NL = KIND == KIND_INT4 ? 1 : 2;       // 16-byte loads per tile-step
-  static constexpr int D = (KIND == KIND_INT4 ? (MT == 1 ? MIQ_D1 : 8) : (MT == 1 ? MIQ_D1 / 2 : 4)) / NR;  // ring depth in k-steps
+  // ring depth in k-steps: 8 KiB of weights per wavefront (4 KiB for 3-4 activation
+  // tiles with one weight tile, so that a chunk of D k-steps of activations fits LDS)
+  static constexpr int D = (KIND == KIND_INT4 ? (MT == 1 ? MIQ_D1 : (MT >= 3 && NR == 1 ? 4 : 8))
+                                              : (MT == 1 ? MIQ_D1 / 2 : (MT >= 3 && NR == 1 ? 2 : 4))) / NR;
   static constexpr int XR = 16 * MT;                          // x-sum row pitch
   static constexpr int XP = 4;                                // staging pieces per thread per round
 };
@@ -370,15 +373,18 @@ StreamPlan plan_stream(int kind, int64_t M, int64_t N, int64_t K, int group_step
   pl.unit_steps = kind == KIND_INT4 ? group_steps : 1;
   pl.units = (int)(steps / pl.unit_steps);
   pl.MT = (int)((M + 15) / 16);
-  pl.NR = pl.MT >= 2 ? 2 : 1;
+  // two weight tiles per wavefront (x reused twice from LDS) when there are many rows;
+  // with few rows one tile, which keeps the partials a row block reads back small
+  pl.NR = pl.MT >= 2 && N > 8192 ? 2 : 1;
   int S = 0;
   const char* env = getenv("MIQ_WO_PLAN");  // "NR,S" override for tuning
   int e_nr = 0, e_s = 0;
   if (env && sscanf(env, "%d,%d", &e_nr, &e_s) == 2 && (e_nr == 1 || e_nr == 2) && e_s >= 1) {
-    if ((pl.MT == 2 && e_nr == 2) || (pl.MT < 3 && e_nr == 1)) pl.NR = e_nr;  // D-step chunks must fit LDS
+    if (pl.MT >= 2 || e_nr == 1) pl.NR = e_nr;
     S = e_s;
   }
-  pl.D = (kind == KIND_INT4 ? (pl.MT == 1 ? MIQ_D1 : 8) : (pl.MT == 1 ? MIQ_D1 / 2 : 4)) / pl.NR;  // Cfg<>::D
+  pl.D = (kind == KIND_INT4 ? (pl.MT == 1 ? MIQ_D1 : (pl.MT >= 3 && pl.NR == 1 ? 4 : 8))
+                             : (pl.MT == 1 ? MIQ_D1 / 2 : (pl.MT >= 3 && pl.NR == 1 ? 2 : 4))) / pl.NR;  // Cfg<>::D
   const int64_t rows = (pl.MT == 1 ? waves_for<1>() : waves_for<2>()) * pl.NR * 16;
   pl.blocks = (int)((N + rows - 1) / rows);
   if (S == 0) {
