@@ -28,10 +28,12 @@ def _contig_rows(w):
 # ---------------------------------------------------------------- int8 weight-only
 def int8_quantize(weight, scale_dtype):
     """engine/quantization/int8_wo.py:8-12 -> (q int8 [..., N, K], scale [..., N, 1])."""
-    L.require_device(weight)
-    w2 = _contig_rows(weight)
     q = torch.empty(weight.shape, dtype=torch.int8, device=weight.device)
     scale = torch.empty(weight.shape[:-1] + (1,), dtype=scale_dtype, device=weight.device)
+    if weight.is_meta:  # shapes only (a cache load builds the modules on "meta" first)
+        return q, scale
+    L.require_device(weight)
+    w2 = _contig_rows(weight)
     L.call("miq_int8_quantize", L.ptr(w2), L.dtype_code(w2.dtype), w2.shape[0], w2.shape[1], w2.stride(0),
            L.ptr(q), L.ptr(scale), L.dtype_code(scale_dtype), L.stream(weight.device))
     return q, scale
@@ -74,13 +76,15 @@ def w8a16_supported(x, qweight):
 # ---------------------------------------------------------------- int4 weight-only
 def int4_quantize(weight, group_size, sz_dtype, symmetric=False):
     """int4_wo.py:15-31 -> (packed uint8 [..., N, K/2], scale [..., N, K/g], zero or None)."""
-    L.require_device(weight)
-    w2 = _contig_rows(weight)
-    K = w2.shape[1]
+    K = weight.shape[-1]
     lead = weight.shape[:-1]
     q = torch.empty(lead + (K // 2,), dtype=torch.uint8, device=weight.device)
     scale = torch.empty(lead + (K // group_size,), dtype=sz_dtype, device=weight.device)
     zero = None if symmetric else torch.empty_like(scale)
+    if weight.is_meta:  # shapes only
+        return q, scale, zero
+    L.require_device(weight)
+    w2 = _contig_rows(weight)
     L.call("miq_int4_quantize", L.ptr(w2), L.dtype_code(w2.dtype), w2.shape[0], K, w2.stride(0), group_size,
            L.ptr(q), L.ptr(scale), L.ptr(zero), L.dtype_code(sz_dtype), L.stream(weight.device))
     return q, scale, zero
@@ -132,10 +136,12 @@ def w4a16_supported(x, qweight, scale):
 # ---------------------------------------------------------------- fp8 weight + activation
 def fp8_quantize_rows(x):
     """fp8.py:32-36 / 41-46 -> (e4m3fn [..., K], fp32 scale [...])."""
-    L.require_device(x)
-    x2 = _contig_rows(x)
     q = torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=x.device)
     scale = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+    if x.is_meta:  # shapes only
+        return q, scale
+    L.require_device(x)
+    x2 = _contig_rows(x)
     L.call("miq_fp8_quantize_rows", L.ptr(x2), L.dtype_code(x2.dtype), x2.shape[0], x2.shape[1], x2.stride(0),
            L.ptr(q), L.ptr(scale), L.stream(x.device))
     return q, scale
