@@ -35,6 +35,11 @@ FP8_PEAK_TFLOPS = 5000.0     # MI355X dense FP8 MFMA, published
 ROTATE_BYTES = 600 * 2 ** 20  # > 2 x MALL
 METRIC = "quantized decode GEMM GB/s (% HBM peak) at M=1..64; FP8-KV attn µs/step"
 MS = (1, 8, 32, 64)
+# HBM bytes per headline launch (mean over M = 1, 8, 32, 64), from rocprofv3 FETCH_SIZE /
+# WRITE_SIZE passes of `bench.py --only headline --copy-probe`, scaled by the counters'
+# readings for a 256 MiB sum and fill (profiles/wo_stream_int4_headline_traffic.md).
+# Re-measure when the kernel changes.
+HEADLINE_TRAFFIC_BYTES = 22_854_035
 
 
 def log(*a):
@@ -378,7 +383,8 @@ def main():
         "config": {"workload": "INT4 W4A16 decode GEMM, Qwen3-4B down_proj N=2560 K=9728, group 128 symmetric, "
                                "one step = M in {1,8,32,64}", "global_batch": list(MS), "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": HEADLINE_TRAFFIC_BYTES,
+                     "traffic_unit": "bytes per launch", "algorithmic_bytes_per_launch": round(step_bytes / 4),
                      "kernel": "wo_stream_kernel<KIND_INT4>", "avg_kernel_us": round(avg_kernel_us, 3)},
         "cpu_baseline": cpu,
         "breakdown": breakdown,

@@ -646,24 +646,48 @@ paged_decode_split8_kernel(AttnParams p) {
   MIQ_TRACE(4);
 }
 
-// out[b, h] = sum_s exp(lse_s - max) o_s / sum_s exp(lse_s - max)
+// out[b, h] = sum_s exp(lse_s - max) o_s / sum_s exp(lse_s - max). The weights of the
+// partitions are computed once per workgroup from LDS; the partial rows are read 4 at a
+// time so their loads are in flight together.
 __global__ void __launch_bounds__(kD)
 paged_decode_merge_kernel(const float* __restrict__ o_part, const float* __restrict__ lse_part,
                           const int32_t* __restrict__ lens, int H, int partition, int max_parts,
                           uint16_t* __restrict__ out, int64_t os_b, int64_t os_h) {
+  __shared__ float s_w[kD];
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int L = lens[b];
   int np = (L + partition - 1) / partition;
   if (np < 1) np = 1;
   if (np > max_parts) np = max_parts;  // a context longer than the caller's max_len is cut
   const int64_t base = ((int64_t)b * H + h) * max_parts;
-  float mx = -__builtin_inff();
-  for (int s = 0; s < np; ++s) mx = fmaxf(mx, lse_part[base + s]);
-  float num = 0.f, den = 0.f;
-  if (mx != -__builtin_inff()) {
-    for (int s = 0; s < np; ++s) {
-      const float w = __expf(lse_part[base + s] - mx);
-      num += w * o_part[(base + s) * kD + d];
+  float mx = -__builtin_inff(), den = 0.f, num = 0.f;
+  for (int s0 = 0; s0 < np; s0 += kD) {  // kD partitions per round (one per thread)
+    const int cnt = min(kD, np - s0);
+    __syncthreads();
+    if (d < cnt) s_w[d] = lse_part[base + s0 + d];
+    __syncthreads();
+    float m2 = mx;
+    for (int i = 0; i < cnt; ++i) m2 = fmaxf(m2, s_w[i]);
+    if (m2 == -__builtin_inff()) continue;
+    const float rescale = __expf(mx - m2);  // exp(-inf) = 0 on the first round
+    num *= rescale;
+    den *= rescale;
+    mx = m2;
+    int i = 0;
+    for (; i + 4 <= cnt; i += 4) {
+      float o4[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) o4[u] = o_part[(base + s0 + i + u) * kD + d];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float w = __expf(s_w[i + u] - mx);
+        num += w * o4[u];
+        den += w;
+      }
+    }
+    for (; i < cnt; ++i) {
+      const float w = __expf(s_w[i] - mx);
+      num += w * o_part[(base + s0 + i) * kD + d];
       den += w;
     }
   }
