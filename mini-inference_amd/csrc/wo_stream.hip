@@ -134,6 +134,9 @@ wo_stream_kernel(StreamParams p) {
   // branches cost the precise waits)
   int nsteps_v = st1 - st0;
   asm volatile("" : "+v"(nsteps_v));
+  // quantization group of the next request, and its k-steps still to request (requests
+  // come in k order), kept as uniform counters instead of divisions
+  int rq_grp = 0, rq_left = p.group_steps;
   auto request = [&](int d, int kl) {  // k-step st0 + kl into slot d
     const int keep = (kl - nsteps_v) >> 31;  // all ones while kl < steps in range
 #pragma unroll
@@ -145,24 +148,31 @@ wo_stream_kernel(StreamParams p) {
         wq[d][t][L] = *reinterpret_cast<const uint4*>(&v);
       }
       if (KIND == KIND_INT4) {
-        const int gi = soff[t] + kl / p.group_steps;
+        const int gi = soff[t] + rq_grp;
         constexpr int esz = SD == MIQ_F32 ? 4 : 2;
         const int so = ((gi * esz) & ~3 & keep) | (kOut & ~keep);
         sq[d][t] = __builtin_amdgcn_raw_buffer_load_b32(srs, so, 0, 0);
         zq[d][t] = HZ ? __builtin_amdgcn_raw_buffer_load_b32(zrs, so, 0, 0) : 0u;
       }
     }
+    if (--rq_left == 0) {
+      ++rq_grp;
+      rq_left = p.group_steps;
+    }
   };
 #pragma unroll
   for (int d = 0; d < D; ++d) request(d, d);
   MIQ_TRACE(1);
 
-  f32x4 acc[NR][MT], accg[NR][MT], xsg[MT];
+  // two MFMA accumulation chains per tile (even / odd j), so consecutive MFMAs do not
+  // wait for each other's results
+  f32x4 acc[NR][MT], accg[NR][MT], acc2[NR][MT], xsg[MT];
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int t = 0; t < NR; ++t)
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) { acc[t][mt] = z4; accg[t][mt] = z4; }
+    for (int mt = 0; mt < MT; ++mt) { acc[t][mt] = z4; accg[t][mt] = z4; acc2[t][mt] = z4; }
+  int c_grp = 0, c_left = p.group_steps;  // the multiply loop's group and steps left in it
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) xsg[mt] = z4;
 
@@ -230,25 +240,28 @@ wo_stream_kernel(StreamParams p) {
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
               for (int j = 0; j < 4; ++j) {
-                if (KIND == KIND_INT4) accg[t][mt] = mfma(av[mt][j], bv[j], accg[t][mt]);
-                else acc[t][mt] = mfma(av[mt][j], bv[j], acc[t][mt]);
+                f32x4& chain = (j & 1) ? acc2[t][mt] : (KIND == KIND_INT4 ? accg[t][mt] : acc[t][mt]);
+                chain = mfma(av[mt][j], bv[j], chain);
               }
           }
-          if (KIND == KIND_INT4 && (kst + 1) % p.group_steps == 0) {  // end of a quantization group
+          if (KIND == KIND_INT4 && --c_left == 0) {  // end of a quantization group
 #pragma unroll
             for (int t = 0; t < NR; ++t) {
-              const int gi = soff[t] + (kst - st0) / p.group_steps;
+              const int gi = soff[t] + c_grp;
               const float sc = word_to_f32<SD>(sq[d][t], gi);
               const float cz = HZ ? word_to_f32<SD>(zq[d][t], gi) - 128.f * sc : -136.f * sc;
 #pragma unroll
               for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-                for (int v = 0; v < 4; ++v) acc[t][mt][v] += sc * accg[t][mt][v] + cz * xsg[mt][v];
+                for (int v = 0; v < 4; ++v) acc[t][mt][v] += sc * (accg[t][mt][v] + acc2[t][mt][v]) + cz * xsg[mt][v];
                 accg[t][mt] = z4;
+                acc2[t][mt] = z4;
               }
             }
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) xsg[mt] = z4;
+            ++c_grp;
+            c_left = p.group_steps;
           }
         }
         request(d, kst + D - st0);
@@ -261,7 +274,7 @@ wo_stream_kernel(StreamParams p) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[t][mt][v] -= 128.f * xsg[mt][v];
+        for (int v = 0; v < 4; ++v) acc[t][mt][v] += acc2[t][mt][v] - 128.f * xsg[mt][v];
   }
 
   MIQ_TRACE(3);
