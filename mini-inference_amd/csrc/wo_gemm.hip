@@ -2,7 +2,8 @@
 //
 //   y[m, n] = sum_k x[m, k] * W[n, k],  x bf16 [M, K],  W int8 [N, K] or int4 [N, K/2]
 //
-// Argument checks live here; the kernel and its plan are in wo_stream.hip.
+// Argument checks live here. Up to 16 rows whose activations fit LDS run the one-tile-per-
+// workgroup kernel (wo_tile.hip); the rest the streamed split-K kernel (wo_stream.hip).
 #include "wo_core.h"
 
 namespace miq {
@@ -11,6 +12,9 @@ size_t wo_stream_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bit
 int wo_stream_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, const void* scale,
                      const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int M,
                      int N, int K, void* workspace, size_t ws_bytes, hipStream_t st, const char* name);
+int wo_tile_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, const void* scale,
+                   const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int M,
+                   int N, int K, hipStream_t st, const char* name, bool& launched);
 
 namespace {
 
@@ -39,6 +43,10 @@ int run(int kind, const WoArgs& p, void* workspace, size_t ws_bytes, hipStream_t
               "%s: x must be 16-byte aligned with a row stride multiple of 8", name);
   MIQ_REQUIRE((reinterpret_cast<uintptr_t>(p.w) & 15) == 0, "%s: weights must be 16-byte aligned", name);
   MIQ_REQUIRE(p.ldx >= p.K && p.ldy >= p.N, "%s: bad strides", name);
+  bool launched = false;
+  const int rc = wo_tile_launch(kind, p.x, p.ldx, p.w, p.ldw, p.scale, p.zero, p.sz_dtype, p.group_steps, p.ngroups,
+                                p.y, p.ldy, p.M, p.N, p.K, st, name, launched);
+  if (launched || rc != MIQ_OK) return rc;
   return wo_stream_launch(kind, p.x, p.ldx, p.w, p.ldw, p.scale, p.zero, p.sz_dtype, p.group_steps, p.ngroups, p.y,
                           p.ldy, p.M, p.N, p.K, workspace, ws_bytes, st, name);
 }

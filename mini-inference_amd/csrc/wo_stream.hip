@@ -31,6 +31,8 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "wo_core.h"
 
 #ifndef MIQ_TRACE
@@ -40,7 +42,7 @@
 // ring depth (k-steps of int4 weights in flight per wavefront) for one activation tile;
 // 8 and 16 measured the same or 8 slightly better on the decode shapes
 #ifndef MIQ_D1
-#define MIQ_D1 8
+#define MIQ_D1 4
 #endif
 
 namespace miq {
@@ -112,12 +114,21 @@ wo_stream_kernel(StreamParams p) {
   // this wavefront's weight rows (rows past N re-read row N - 1; never stored) and the
   // byte offsets of their k-step st0 in the weight / scale buffers
   const int nblk0 = blockIdx.x * (kWaves * NR * 16);
-  int nrow[NR], woff[NR], soff[NR];
+  // Weight loads read whole 128-byte lines: load h of a tile covers its rows 8h..8h+7, 128
+  // bytes each (two int4 k-steps, one int8 k-step); lane (g, r) reads row 8h + (r & 7),
+  // 16-byte chunk ch[h] = ((r >> 3) ^ h) * 4 + g. swizzle() turns the two loads into the
+  // per-k-step MFMA layout (lane (g, r): row r, chunk g of each 64-byte half).
+  int nrow[NR], woff[NR][2], soff[NR];
+  const int ch[2] = {(r >> 3) * 4 + g, ((r >> 3) ^ 1) * 4 + g};
 #pragma unroll
   for (int t = 0; t < NR; ++t) {
     nrow[t] = nblk0 + (wv * NR + t) * 16 + r;
     const int nc = min(nrow[t], p.N - 1);
-    woff[t] = nc * (int)p.ldw + st0 * kStepBytes + g * 16;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int nh = min(nblk0 + (wv * NR + t) * 16 + 8 * h + (r & 7), p.N - 1);
+      woff[t][h] = nh * (int)p.ldw + st0 * kStepBytes + ch[h] * 16;
+    }
     soff[t] = (int)(nc * p.ngroups + st0 / p.group_steps);  // element index of the first group
   }
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.w), 0, p.wbytes, 0x00020000);
@@ -137,15 +148,22 @@ wo_stream_kernel(StreamParams p) {
   // quantization group of the next request, and its k-steps still to request (requests
   // come in k order), kept as uniform counters instead of divisions
   int rq_grp = 0, rq_left = p.group_steps;
+  // int4: the raw loads of k-steps d and d + 1 (d even) sit in wq[d][t][0] and wq[d + 1][t][0];
+  // int8: those of k-step d in wq[d][t][0..1]
   auto request = [&](int d, int kl) {  // k-step st0 + kl into slot d
     const int keep = (kl - nsteps_v) >> 31;  // all ones while kl < steps in range
 #pragma unroll
     for (int t = 0; t < NR; ++t) {
+      if (KIND == KIND_INT8 || (d & 1) == 0) {
 #pragma unroll
-      for (int L = 0; L < NL; ++L) {
-        const int off = ((woff[t] + kl * kStepBytes + L * 64) & keep) | (kOut & ~keep);
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2 /* nt */);
-        wq[d][t][L] = *reinterpret_cast<const uint4*>(&v);
+        for (int h = 0; h < 2; ++h) {
+          // int4 chunks 4..7 hold k-step kl + 1
+          const int kp = KIND == KIND_INT4 ? (kl + (ch[h] >> 2) - nsteps_v) >> 31 : keep;
+          const int off = ((woff[t][h] + kl * kStepBytes) & kp) | (kOut & ~kp);
+          const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2 /* nt */);
+          if (KIND == KIND_INT4) wq[d + h][t][0] = *reinterpret_cast<const uint4*>(&v);
+          else wq[d][t][h] = *reinterpret_cast<const uint4*>(&v);
+        }
       }
       if (KIND == KIND_INT4) {
         const int gi = soff[t] + rq_grp;
@@ -160,9 +178,47 @@ wo_stream_kernel(StreamParams p) {
       rq_left = p.group_steps;
     }
   };
+  static_assert(KIND == KIND_INT8 || D % 2 == 0, "int4 loads come in pairs of k-steps");
+
+  // LDS: x chunk [M rows x (CS * 128 + 8)] bf16, then [CS][XR] fp32 sums per k-step
+  const int CS = p.chunk_steps;
+  const int xstride = CS * kStepK + 8;
+  float* xsum = reinterpret_cast<float*>(lds + M * xstride);
+  const int xld = (int)(p.ldx / 8);
+  // activation pieces (16 bytes) of chunk c0, round `base`: XP per thread; pieces j of a
+  // round that no thread needs are not loaded (a uniform branch)
+  uint4 xr[XP];
+  auto load_x = [&](int c0, int base) {
+    const int xcols = min(CS, st1 - c0) * (kStepK / 8);
+    const int npieces = M * xcols;
+    const uint4* xsrc = reinterpret_cast<const uint4*>(p.x) + (int64_t)c0 * (kStepK / 8);
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      if (base + j * kThreads < npieces) {
+        const int i = min(base + tid + j * kThreads, npieces - 1);
+        const int m = i / xcols, c = i - m * xcols;
+        xr[j] = xsrc[(int64_t)m * xld + c];
+      }
+    }
+  };
+  // the first activations are requested ahead of the weights: loads complete in order, so
+  // staging them does not wait for the weights
+  load_x(st0, 0);
 #pragma unroll
   for (int d = 0; d < D; ++d) request(d, d);
   MIQ_TRACE(1);
+  // lanes r < 8 keep load 0 for the first half and take load 1's second half from lane
+  // r + 8; lanes r >= 8 the other way round (a DPP row rotation by 8)
+  const bool lo_half = r < 8;
+  auto swizzle = [&](const uint4& i0, const uint4& i1, uint4& f0, uint4& f1) {
+    const uint4 a = lo_half ? i0 : i1, b = lo_half ? i1 : i0;
+    f0 = a;
+    f1.x = __builtin_amdgcn_update_dpp(0u, b.x, 0x128, 0xf, 0xf, false);
+    f1.y = __builtin_amdgcn_update_dpp(0u, b.y, 0x128, 0xf, 0xf, false);
+    f1.z = __builtin_amdgcn_update_dpp(0u, b.z, 0x128, 0xf, 0xf, false);
+    f1.w = __builtin_amdgcn_update_dpp(0u, b.w, 0x128, 0xf, 0xf, false);
+  };
+  uint4 wnext[NR];  // int4: the second k-step of the pair being multiplied
 
   // two MFMA accumulation chains per tile (even / odd j), so consecutive MFMAs do not
   // wait for each other's results
@@ -176,28 +232,16 @@ wo_stream_kernel(StreamParams p) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) xsg[mt] = z4;
 
-  // LDS: x chunk [M rows x (CS * 128 + 8)] bf16, then [CS][XR] fp32 sums per k-step
-  const int CS = p.chunk_steps;
-  const int xstride = CS * kStepK + 8;
-  float* xsum = reinterpret_cast<float*>(lds + M * xstride);
-  const int xld = (int)(p.ldx / 8);
-
   for (int c0 = st0; c0 < st1; c0 += CS) {
     const int nst = min(CS, st1 - c0);
     const int xcols = nst * (kStepK / 8);  // 16-byte pieces per activation row
     const int npieces = M * xcols;
-    const uint4* xsrc = reinterpret_cast<const uint4*>(p.x) + (int64_t)c0 * (kStepK / 8);
     if (c0 != st0) __syncthreads();  // every wavefront is done with the previous chunk
     for (int base = 0; base < npieces; base += XP * kThreads) {
-      uint4 xr[XP];
+      if (c0 != st0 || base != 0) load_x(c0, base);
 #pragma unroll
       for (int j = 0; j < XP; ++j) {
-        const int i = min(base + tid + j * kThreads, npieces - 1);
-        const int m = i / xcols, c = i - m * xcols;
-        xr[j] = xsrc[(int64_t)m * xld + c];
-      }
-#pragma unroll
-      for (int j = 0; j < XP; ++j) {
+        if (base + j * kThreads >= npieces) break;
         const int i = base + tid + j * kThreads;
         const int ic = min(i, npieces - 1);
         const int m = ic / xcols, c = ic - m * xcols;
@@ -235,7 +279,15 @@ wo_stream_kernel(StreamParams p) {
 #pragma unroll
           for (int t = 0; t < NR; ++t) {
             bf16x8 bv[4];
-            unpack_b<KIND>(wq[d][t], bv);
+            uint4 wl[2];
+            if (KIND == KIND_INT8) {
+              swizzle(wq[d][t][0], wq[d][t][1], wl[0], wl[1]);
+            } else if ((d & 1) == 0) {
+              swizzle(wq[d][t][0], wq[d + 1][t][0], wl[0], wnext[t]);
+            } else {
+              wl[0] = wnext[t];
+            }
+            unpack_b<KIND>(wl, bv);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -384,6 +436,9 @@ StreamPlan plan_stream(int kind, int64_t M, int64_t N, int64_t K, int group_step
   StreamPlan pl{};
   const int64_t steps = K / kStepK;
   pl.unit_steps = kind == KIND_INT4 ? group_steps : 1;
+  // int4 splits start on an even k-step when they can, so each weight load covers whole
+  // 128-byte lines
+  if (kind == KIND_INT4 && group_steps % 2 == 1 && steps % (2 * group_steps) == 0) pl.unit_steps = 2 * group_steps;
   pl.units = (int)(steps / pl.unit_steps);
   pl.MT = (int)((M + 15) / 16);
   // two weight tiles per wavefront (x reused twice from LDS) when there are many rows;
@@ -403,8 +458,14 @@ StreamPlan plan_stream(int kind, int64_t M, int64_t N, int64_t K, int group_step
   if (S == 0) {
     // about 2 workgroups per CU for one tile of activation rows, about 1.5 for more
     // rows (measured on MI355X over the Qwen3 projection shapes)
-    if (pl.MT == 1) S = (int)((512 + pl.blocks - 1) / pl.blocks);
-    else S = (int)((400 + pl.blocks / 2) / pl.blocks);
+    // one activation tile: splits of about 8 k-steps; more tiles: about 1.5 workgroups
+    // per CU (measured on MI355X over the Qwen3 projection shapes)
+    if (pl.MT == 1) {
+      const int per = std::max(1, 8 / pl.unit_steps);
+      S = (pl.units + per - 1) / per;
+    } else {
+      S = (int)((400 + pl.blocks / 2) / pl.blocks);
+    }
     if (S < 1) S = 1;
   }
   if (S > pl.units) S = pl.units;

@@ -1,0 +1,388 @@
+// Weight-only quantized GEMM for decode (1 <= M <= 16 activation rows), one weight tile
+// per workgroup:
+//
+//   y[m, n] = sum_k x[m, k] * W[n, k],  x bf16 [M, K],  W int8 [N, K] or int4 [N, K/2]
+//
+// A workgroup of W wavefronts owns one tile of 16 weight rows over the whole K; the K
+// range is cut into W slices of whole quantization groups, one per wavefront. Every
+// wavefront requests its whole slice of weights (at most 8 k-steps, 8 KiB) and scales at
+// once, right after the activation loads, so a wavefront sees one memory round trip
+// instead of a ring of them. The activations (all of K) are staged in LDS once per
+// workgroup; the W partial tiles are added through LDS in wavefront order, so there is
+// no split-K workspace, no cross-workgroup counter and no second round trip for partial
+// sums. A launch has N / 16 workgroups of 4 to 16 wavefronts.
+//
+// Per-element math is the one of the streamed kernel (wo_stream.hip): codes unpack to
+// bf16 128 + code, MFMA 16x16x32 bf16 with fp32 accumulation in two chains, per-group
+// scales applied as acc += s * accg + (z - 128 s) * sum(x) (int4; -136 s for symmetric
+// codes) and acc - 128 * sum(x) then the row scale for int8.
+//
+// Weight loads read whole 128-byte lines: load h of the tile covers its rows 8h .. 8h + 7,
+// 128 bytes each (two int4 k-steps or one int8 k-step); a DPP row rotation then gives
+// every lane (g, r) row r, chunk g of each 64-byte half, the MFMA B layout.
+#include <algorithm>
+#include <cstdlib>
+
+#include "miq_common.h"
+#include "wo_core.h"
+
+#ifndef MIQ_TRACE
+#define MIQ_TRACE(point)  // per-wavefront timestamps in probe builds
+#endif
+
+namespace miq {
+namespace {
+
+using namespace wo;
+
+constexpr int kTileNS = 8;                 // k-steps in flight per wavefront (all of its slice)
+constexpr int kTileLds = 160 * 1024;       // gfx950 LDS per workgroup
+constexpr int kCUs = 256;                  // MI355X compute units
+// activation pieces (16 B) per thread per round (int8 holds twice the weight registers)
+template <int KIND>
+constexpr int tile_xp() { return KIND == KIND_INT4 ? 8 : 4; }
+
+struct TileParams {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint8_t* w;
+  int64_t ldw;          // bytes per weight row
+  const void* scale;
+  const void* zero;
+  int group_steps;      // int4: k-steps per quantization group (1 for int8)
+  int64_t ngroups;      // int4: groups per weight row
+  uint16_t* y;
+  int64_t ldy;
+  int M, N, steps;      // steps = K / 128
+  int units, unit_steps;
+  int wbytes, sbytes;
+};
+
+template <int KIND, bool HZ, int SD, int W>
+__global__ void __launch_bounds__(W * 64)
+wo_tile_kernel(TileParams p) {
+  constexpr int kThreads = W * 64, NS = kTileNS, XP = tile_xp<KIND>();
+  constexpr int kStepBytes = KIND == KIND_INT4 ? kStepK / 2 : kStepK;  // per weight row
+  extern __shared__ __align__(16) uint16_t lds[];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int M = p.M;
+  MIQ_TRACE(0);
+
+  // this wavefront's slice of K, in whole units (groups, or pairs of them)
+  const int u0 = p.units * wv / W, u1 = p.units * (wv + 1) / W;
+  const int st0 = u0 * p.unit_steps, nst = (u1 - u0) * p.unit_steps;
+
+  // ---- activation loads first (the whole K for M rows), round 0 into registers
+  const int xcols = p.steps * (kStepK / 8);  // 16-byte pieces per activation row
+  const int npieces = M * xcols;
+  const int xld = (int)(p.ldx / 8);
+  const uint4* xsrc = reinterpret_cast<const uint4*>(p.x);
+  uint4 xr[XP];
+  // rounds of XP pieces per thread; pieces j of a round that no thread needs are not
+  // loaded (a uniform branch)
+  auto load_x = [&](int base) {
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      if (base + j * kThreads + wv * 64 < npieces) {  // this wavefront has pieces
+        const int i = min(base + tid + j * kThreads, npieces - 1);
+        const int m = i / xcols, c = i - m * xcols;
+        xr[j] = xsrc[(int64_t)m * xld + c];
+      }
+    }
+  };
+  load_x(0);
+  MIQ_TRACE(5);
+
+  // ---- then every weight and scale word of the slice
+  const int n0 = blockIdx.x * 16;
+  const int nrow = n0 + r;
+  const int ch[2] = {(r >> 3) * 4 + g, ((r >> 3) ^ 1) * 4 + g};
+  int woff[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+    woff[h] = min(n0 + 8 * h + (r & 7), p.N - 1) * (int)p.ldw + st0 * kStepBytes + ch[h] * 16;
+  const int soff = (int)(min(nrow, p.N - 1) * p.ngroups + st0 / p.group_steps);
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.w), 0, p.wbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.scale), 0, p.sbytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t zrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(HZ ? p.zero : p.scale), 0, p.sbytes, 0x00020000);
+  constexpr int kOut = 0x7ffffff0;  // an offset outside every buffer: the load returns zeros
+  // steps of the slice as an opaque per-lane value: loads past it are steered to kOut with
+  // bit operations (a select would become a branch around each load)
+  int nsteps_v = nst;
+  asm volatile("" : "+v"(nsteps_v));
+  // int4: raw loads of k-steps d, d + 1 (d even) in wq[d], wq[d + 1]; int8: wq[d][0..1]
+  constexpr int NL = KIND == KIND_INT4 ? 1 : 2;
+  uint4 wq[NS][NL];
+#pragma unroll
+  for (int d = 0; d < NS; ++d) {
+    if (KIND == KIND_INT8 || (d & 1) == 0) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int kp = (d + (KIND == KIND_INT4 ? (ch[h] >> 2) : 0) - nsteps_v) >> 31;
+        const int off = ((woff[h] + d * kStepBytes) & kp) | (kOut & ~kp);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2 /* nt */);
+        if (KIND == KIND_INT4) wq[d + h][0] = *reinterpret_cast<const uint4*>(&v);
+        else wq[d][h] = *reinterpret_cast<const uint4*>(&v);
+      }
+    }
+  }
+  // int4: the scale (and zero) words of the slice's groups, at most NS of them, with two
+  // 16-byte loads from the aligned word holding the first one
+  constexpr int esz = SD == MIQ_F32 ? 4 : 2;
+  uint32_t sw[8], zw[8];
+  const int sbase = (soff * esz) & ~3;
+  if (KIND == KIND_INT4) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(srs, sbase + 16 * h, 0, 0);
+      const uint4 u = *reinterpret_cast<const uint4*>(&v);
+      sw[4 * h] = u.x; sw[4 * h + 1] = u.y; sw[4 * h + 2] = u.z; sw[4 * h + 3] = u.w;
+      if (HZ) {
+        const auto vz = __builtin_amdgcn_raw_buffer_load_b128(zrs, sbase + 16 * h, 0, 0);
+        const uint4 uz = *reinterpret_cast<const uint4*>(&vz);
+        zw[4 * h] = uz.x; zw[4 * h + 1] = uz.y; zw[4 * h + 2] = uz.z; zw[4 * h + 3] = uz.w;
+      }
+    }
+  }
+  // value of group e (0-based in the slice) from those words: for 16-bit scales the first
+  // group sits in the high half of word 0 when soff is odd
+  const bool odd = esz == 2 && (soff & 1);
+  auto group_value = [&](const uint32_t* wds, int e) -> float {
+    if constexpr (SD == MIQ_F32) {
+      return __builtin_bit_cast(float, wds[e]);
+    } else {
+      const uint32_t even = (e & 1) ? (wds[e >> 1] >> 16) : (wds[e >> 1] & 0xffffu);
+      const uint32_t oddv = ((e + 1) & 1) ? (wds[(e + 1) >> 1] >> 16) : (wds[(e + 1) >> 1] & 0xffffu);
+      return sd_to_f32<SD>(odd ? oddv : even);
+    }
+  };
+
+  MIQ_TRACE(1);
+  // ---- stage the activations: LDS x [M][K + 8] bf16 (int4: pieces permuted for the
+  // unpack order), then xsum [steps][16] fp32, the sum of each row over each k-step
+  const int xstride = p.steps * kStepK + 8;
+  float* xsum = reinterpret_cast<float*>(lds + M * xstride);
+  for (int base = 0; base < npieces; base += XP * kThreads) {
+    if (base != 0) load_x(base);
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+      if (base + j * kThreads + wv * 64 >= npieces) break;  // no pieces loaded for this wavefront
+      const int i = base + tid + j * kThreads;
+      const int ic = min(i, npieces - 1);
+      const int m = ic / xcols, c = ic - m * xcols;
+      *reinterpret_cast<uint4*>(lds + m * xstride + c * 8) = KIND == KIND_INT4 ? permute_for_u4(xr[j]) : xr[j];
+      // 16 consecutive lanes (one DPP row) hold the 16 pieces of one k-step of one row
+      float sm = sum8_bf16(xr[j]);
+      sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x111, 0xf, 0xf, true));
+      sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x112, 0xf, 0xf, true));
+      sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x114, 0xf, 0xf, true));
+      sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x118, 0xf, 0xf, true));
+      if (i < npieces && (c & 15) == 15) xsum[(c >> 4) * 16 + m] = sm;
+    }
+  }
+  __syncthreads();
+  MIQ_TRACE(2);
+
+  // ---- multiply the slice
+  const bool lo_half = r < 8;
+  auto swizzle = [&](const uint4& i0, const uint4& i1, uint4& f0, uint4& f1) {
+    const uint4 a = lo_half ? i0 : i1, b = lo_half ? i1 : i0;
+    f0 = a;
+    f1.x = __builtin_amdgcn_update_dpp(0u, b.x, 0x128, 0xf, 0xf, false);
+    f1.y = __builtin_amdgcn_update_dpp(0u, b.y, 0x128, 0xf, 0xf, false);
+    f1.z = __builtin_amdgcn_update_dpp(0u, b.z, 0x128, 0xf, 0xf, false);
+    f1.w = __builtin_amdgcn_update_dpp(0u, b.w, 0x128, 0xf, 0xf, false);
+  };
+  const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = z4, accg = z4, acc2 = z4, xsg = z4;
+  int c_grp = 0, c_left = p.group_steps;
+  const uint16_t* xrow = lds + min(r, M - 1) * xstride;
+  uint4 wnext;
+#pragma unroll
+  for (int d = 0; d < NS; ++d) {
+    if (d < nst) {
+      const int kl = st0 + d;
+      bf16x8 av[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xrow + a_off<KIND>(kl, g, j));
+        av[j] = as_bf16x8(v.x, v.y, v.z, v.w);
+      }
+      xsg += *reinterpret_cast<const f32x4*>(xsum + kl * 16 + g * 4);
+      uint4 wl[2];
+      if (KIND == KIND_INT8) {
+        swizzle(wq[d][0], wq[d][1], wl[0], wl[1]);
+      } else if ((d & 1) == 0) {
+        swizzle(wq[d][0], wq[d + 1][0], wl[0], wnext);
+      } else {
+        wl[0] = wnext;
+      }
+      bf16x8 bv[4];
+      unpack_b<KIND>(wl, bv);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        f32x4& chain = (j & 1) ? acc2 : (KIND == KIND_INT4 ? accg : acc);
+        chain = mfma(av[j], bv[j], chain);
+      }
+      if (KIND == KIND_INT4 && --c_left == 0) {  // end of a quantization group
+        // group d of the slice for one-step groups (a compile-time index), else c_grp
+        // picked by a select chain (a run-time index into the word array would spill it)
+        float sc, zv = 0.f;
+        if (p.group_steps == 1) {
+          sc = group_value(sw, d);
+          if (HZ) zv = group_value(zw, d);
+        } else {
+          sc = group_value(sw, 0);
+          if (HZ) zv = group_value(zw, 0);
+#pragma unroll
+          for (int e = 1; e < NS; ++e) {
+            if (e > d) break;
+            sc = c_grp == e ? group_value(sw, e) : sc;
+            if (HZ) zv = c_grp == e ? group_value(zw, e) : zv;
+          }
+        }
+        const float cz = HZ ? zv - 128.f * sc : -136.f * sc;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[v] += sc * (accg[v] + acc2[v]) + cz * xsg[v];
+        accg = z4;
+        acc2 = z4;
+        xsg = z4;
+        ++c_grp;
+        c_left = p.group_steps;
+      }
+    }
+  }
+  if (KIND == KIND_INT8) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[v] += acc2[v] - 128.f * xsg[v];
+  }
+
+  MIQ_TRACE(3);
+  // ---- add the W partial tiles in wavefront order: red [W][M][16] fp32 over the x area
+  __syncthreads();  // every wavefront is done reading the activations
+  float* red = reinterpret_cast<float*>(lds);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int m = g * 4 + v;  // lane (r, g) holds y[4 g + v][n0 + r]
+    if (m < M) red[(wv * M + m) * 16 + r] = acc[v];
+  }
+  __syncthreads();
+  for (int t = tid; t < M * 16; t += kThreads) {
+    const int m = t >> 4, n = n0 + (t & 15);
+    if (n >= p.N) continue;
+    float o = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) o += red[w * M * 16 + t];
+    if (KIND == KIND_INT8)
+      o = bf16_to_f32(f32_to_bf16(o)) * bf16_to_f32(f32_to_bf16(sd_to_f32<SD>(load_sd_raw<SD>(p.scale, n))));
+    p.y[(int64_t)m * p.ldy + n] = f32_to_bf16(o);
+  }
+  MIQ_TRACE(4);
+}
+
+template <int KIND, bool HZ, int SD, int W>
+void launch_tile(const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
+  static bool attr = false;
+  if (!attr) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wo_tile_kernel<KIND, HZ, SD, W>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, kTileLds);
+    attr = true;
+  }
+  hipLaunchKernelGGL((wo_tile_kernel<KIND, HZ, SD, W>), dim3(blocks), dim3(W * 64), lds, st, p);
+}
+
+template <int KIND, bool HZ, int SD>
+void launch_w(int W, const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
+  if (W == 4) launch_tile<KIND, HZ, SD, 4>(p, blocks, lds, st);
+  else if (W == 8) launch_tile<KIND, HZ, SD, 8>(p, blocks, lds, st);
+  else launch_tile<KIND, HZ, SD, 16>(p, blocks, lds, st);
+}
+
+template <int KIND, bool HZ>
+void launch_tile_sd(int sd, int W, const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
+  if (sd == MIQ_BF16) launch_w<KIND, HZ, MIQ_BF16>(W, p, blocks, lds, st);
+  else if (sd == MIQ_F16) launch_w<KIND, HZ, MIQ_F16>(W, p, blocks, lds, st);
+  else launch_w<KIND, HZ, MIQ_F32>(W, p, blocks, lds, st);
+}
+
+}  // namespace
+
+// The tile plan for (M, N, K): wavefronts per workgroup W (0 = the tile kernel does not
+// apply: more than 16 rows, a slice longer than 8 k-steps, or activations too large for
+// LDS), the unit of K slicing and the LDS bytes.
+struct TilePlan {
+  int W, units, unit_steps;
+  size_t lds_bytes;
+};
+
+static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_steps) {
+  TilePlan pl{0, 0, 0, 0};
+  if (M < 1 || M > 16 || N < 1 || K < kStepK) return pl;
+  if (getenv("MIQ_WO_STREAM")) return pl;  // force the streamed kernel (tuning, tests)
+  // int8 with more than 2 rows: the streamed kernel measured faster on MI355X (the staged
+  // activations of a tile outweigh the saved round trips there)
+  if (kind == KIND_INT8 && M > 2) return pl;
+  const int64_t steps = K / kStepK;
+  int us = kind == KIND_INT4 ? group_steps : 1;
+  // int4 slices start on an even k-step when they can (whole 128-byte lines per load)
+  if (kind == KIND_INT4 && us % 2 == 1 && steps % (2 * us) == 0) us *= 2;
+  const int64_t units = steps / us;
+  if (us > kTileNS) return pl;
+  const int64_t xbytes = M * (steps * kStepK + 8) * 2;
+  for (int W : {4, 8, 16}) {
+    if ((units + W - 1) / W * us > kTileNS) continue;
+    const size_t lds = (size_t)std::max<int64_t>(xbytes, (int64_t)W * M * 16 * 4) + (size_t)steps * 16 * 4;
+    if (lds > (size_t)kTileLds) return pl;
+    // every tile should be resident at once (a second wave of workgroups would stage the
+    // activations again): workgroups per CU from LDS and from 16 wavefronts per CU
+    const int64_t per_cu = std::min<int64_t>((int64_t)kTileLds / (int64_t)lds, 16 / W);
+    if ((N + 15) / 16 > per_cu * kCUs * 5 / 4) return pl;
+    pl.W = W;
+    pl.units = (int)units;
+    pl.unit_steps = us;
+    pl.lds_bytes = lds;
+    return pl;
+  }
+  return pl;
+}
+
+// Launches the tile kernel when it applies (`launched` says whether it did); returns a
+// MIQ_* status.
+int wo_tile_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, const void* scale,
+                   const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int M,
+                   int N, int K, hipStream_t st, const char* name, bool& launched) {
+  launched = false;
+  const TilePlan pl = plan_tile(kind, M, N, K, group_steps);
+  if (pl.W == 0) return MIQ_OK;
+  MIQ_REQUIRE((int64_t)N * ldw < 0x7fff0000LL, "%s: weights of %lld bytes exceed 2 GiB", name, (long long)N * ldw);
+  TileParams p{};
+  p.x = x;
+  p.ldx = ldx;
+  p.w = w;
+  p.ldw = ldw;
+  p.scale = scale;
+  p.zero = zero;
+  p.group_steps = group_steps;
+  p.ngroups = ngroups;
+  p.y = y;
+  p.ldy = ldy;
+  p.M = M;
+  p.N = N;
+  p.steps = K / kStepK;
+  p.units = pl.units;
+  p.unit_steps = pl.unit_steps;
+  p.wbytes = (int)((int64_t)N * ldw);
+  const int esz = sd == MIQ_F32 ? 4 : 2;
+  p.sbytes = kind == KIND_INT4 ? (int)(((int64_t)N * ngroups * esz + 3) & ~3LL) : 0;
+  const unsigned blocks = (unsigned)((N + 15) / 16);
+  if (kind == KIND_INT8) launch_tile_sd<KIND_INT8, false>(sd, pl.W, p, blocks, pl.lds_bytes, st);
+  else if (zero) launch_tile_sd<KIND_INT4, true>(sd, pl.W, p, blocks, pl.lds_bytes, st);
+  else launch_tile_sd<KIND_INT4, false>(sd, pl.W, p, blocks, pl.lds_bytes, st);
+  launched = true;
+  return check_launch(name);
+}
+
+}  // namespace miq

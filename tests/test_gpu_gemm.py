@@ -119,6 +119,49 @@ def test_w4a16_scale_dtypes(sdt):
     within(y, want)
 
 
+# Up to 16 rows whose activations fit LDS run the one-tile-per-workgroup kernel; the
+# streamed split-K kernel (forced with MIQ_WO_STREAM) must give the same results there.
+# Cases: multi-wavefront slices (K = 9728), an odd number of k-steps (K = 1152), groups of
+# 3 k-steps, long groups, f32 scales.
+TILE_CASES = [(1, 320, 9728, 128), (4, 320, 9728, 128), (3, 160, 1152, 128), (2, 96, 1152, 384),
+              (8, 64, 4096, 512), (16, 64, 1024, 128), (7, 48, 2560, 256)]
+
+
+@pytest.mark.parametrize("kernel", ["auto", "stream"])
+@pytest.mark.parametrize("M,N,K,group", TILE_CASES)
+@pytest.mark.parametrize("sdt,symmetric", [(torch.bfloat16, True), (torch.float32, False), (torch.float16, False)])
+def test_w4a16_tile_and_stream(kernel, M, N, K, group, sdt, symmetric, monkeypatch):
+    from kernels import quant_ops as ops
+    case(f"w4a16 {kernel} M={M} N={N} K={K} g={group} {sdt} sym={symmetric}")
+    if kernel == "stream":
+        monkeypatch.setenv("MIQ_WO_STREAM", "1")
+    w = make_w(N, K, 50)
+    x = make_x(M, K, 51)
+    q = O.int4_quantize_symmetric(w, group) if symmetric else O.int4_quantize(w, group)
+    q["scale"] = q["scale"].to(sdt)
+    if not symmetric:
+        q["zero"] = q["zero"].to(sdt)
+    want = O.int4_linear_fp32(x, **q)
+    y = ops.w4a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV),
+                         None if symmetric else q["zero"].to(DEV))
+    within(y, want)
+
+
+@pytest.mark.parametrize("kernel", ["auto", "stream"])
+@pytest.mark.parametrize("M,N,K", [(1, 19456, 2560), (2, 4096, 2560), (3, 160, 1152), (4, 64, 9728)])
+def test_w8a16_tile_and_stream(kernel, M, N, K, monkeypatch):
+    from kernels import quant_ops as ops
+    case(f"w8a16 {kernel} M={M} N={N} K={K}")
+    if kernel == "stream":
+        monkeypatch.setenv("MIQ_WO_STREAM", "1")
+    w = make_w(N, K, 52)
+    x = make_x(M, K, 53)
+    q = O.int8_quantize(w, torch.float32)
+    want = O.int8_linear_fp32(x, **q)
+    y = ops.w8a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV))
+    within(y, want)
+
+
 def test_split_k_repeated_calls_are_identical():
     """The split-K counters are left at zero: back-to-back calls give identical bytes."""
     from kernels import quant_ops as ops
