@@ -117,11 +117,16 @@ __device__ inline void unpack_b(const uint4* w, bf16x8 b[4]) {
 }
 
 
+// Sum of the 8 bf16 values of a 16-byte piece: four dot products with (1, 1) (exact
+// products, fp32 sums)
 __device__ inline float sum8_bf16(uint4 v) {
-  const float lo = bf16_to_f32(v.x & 0xffff) + bf16_to_f32(v.y & 0xffff) + bf16_to_f32(v.z & 0xffff) +
-                   bf16_to_f32(v.w & 0xffff);
-  const float hi = bf16_to_f32(v.x >> 16) + bf16_to_f32(v.y >> 16) + bf16_to_f32(v.z >> 16) + bf16_to_f32(v.w >> 16);
-  return lo + hi;
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 one = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+  const float a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, v.x), one, 0.f, false);
+  const float b = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, v.z), one, 0.f, false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, v.w), one,
+                                         __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, v.y), one, a, false),
+                                         false) + b;
 }
 
 // The aligned 32-bit word holding element i of a bf16 / f16 / f32 array (a 16-bit load

@@ -201,9 +201,10 @@ wo_stream_kernel(StreamParams p) {
       }
     }
   };
-  // the first activations are requested ahead of the weights: loads complete in order, so
-  // staging them does not wait for the weights
-  load_x(st0, 0);
+  // with one activation tile the first activations are requested ahead of the weights
+  // (loads complete in order, so staging them does not wait for the weights); with more
+  // tiles that measured slower on MI355X
+  if (MT == 1) load_x(st0, 0);
 #pragma unroll
   for (int d = 0; d < D; ++d) request(d, d);
   MIQ_TRACE(1);
@@ -238,7 +239,7 @@ wo_stream_kernel(StreamParams p) {
     const int npieces = M * xcols;
     if (c0 != st0) __syncthreads();  // every wavefront is done with the previous chunk
     for (int base = 0; base < npieces; base += XP * kThreads) {
-      if (c0 != st0 || base != 0) load_x(c0, base);
+      if (MT > 1 || c0 != st0 || base != 0) load_x(c0, base);
 #pragma unroll
       for (int j = 0; j < XP; ++j) {
         if (base + j * kThreads >= npieces) break;
