@@ -37,9 +37,9 @@ METRIC = "quantized decode GEMM GB/s (% HBM peak) at M=1..64; FP8-KV attn µs/st
 MS = (1, 8, 32, 64)
 # HBM bytes per headline launch (mean over M = 1, 8, 32, 64), from rocprofv3 FETCH_SIZE /
 # WRITE_SIZE passes of `bench.py --only headline --copy-probe`, scaled by the counters'
-# readings for a 256 MiB sum and fill (profiles/wo_stream_int4_headline_traffic.md).
+# readings for a 256 MiB sum and fill (profiles/wo_int4_headline_traffic.md).
 # Re-measure when the kernel changes.
-HEADLINE_TRAFFIC_BYTES = 22_854_035
+HEADLINE_TRAFFIC_BYTES = 22_267_607
 
 
 def log(*a):
@@ -385,7 +385,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(value / HBM_PEAK_GBS, 4), "traffic": HEADLINE_TRAFFIC_BYTES,
                      "traffic_unit": "bytes per launch", "algorithmic_bytes_per_launch": round(step_bytes / 4),
-                     "kernel": "wo_stream_kernel<KIND_INT4>", "avg_kernel_us": round(avg_kernel_us, 3)},
+                     "kernel": "wo_tile_kernel<KIND_INT4> (M=1, 8) and wo_stream_kernel<KIND_INT4> (M=32, 64)",
+                     "avg_kernel_us": round(avg_kernel_us, 3)},
         "cpu_baseline": cpu,
         "breakdown": breakdown,
     }
