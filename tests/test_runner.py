@@ -1,0 +1,160 @@
+"""End-to-end greedy decoding through the build's runner (SURVEY "next" row: engine
+integration and end-to-end greedy parity; reference: engine/core/model_runner.py:11-195,
+tests/test_batching.py:25-52, tests/test_models.py:94-118, 152-187).
+
+CPU (no GPU): the runner glue is pinned the way the reference pins its engine: with no
+quantization, fp32 weights, an unquantized cache and the restated attention, greedy
+tokens equal transformers' `generate` exactly (test_models.py:94-118 pattern), for a
+Qwen3 (per-head q/k norm, GQA) and an OLMoE (full-projection q/k norm, fused experts)
+tiny model built locally.
+
+GPU: the product path end to end, on bf16 tiny models with head_dim 128: quantize_model
+(HIP quantizers), the weight-only / FP8 GEMMs, the fused INT4 MoE, the quantize-on-write
+KV kernel and the paged decode kernel. The same codes are run by the CPU restatement
+(oracle/runner.py) in bf16 at the same rounding points as the GPU (quantized linears
+accumulate in fp32 and round their outputs to bf16; the rest of the model is the same
+torch modules in bf16), teacher-forced on the tokens the GPU produced. Bars:
+  * logits: the 99th percentile of |GPU - oracle| over every step's logits is at most
+    P99_TOL (logit std is about 1.1). The maximum is not bounded: in OLMoE a 1-ulp
+    difference in a router logit can swap an expert of one token (measured 0.91 once);
+  * tokens: every generated token is the oracle's argmax, or within NEAR_TIE of the
+    oracle's top logit (a near-tie that rounding may decide either way), and at least 85%
+    of them are the oracle's argmax exactly.
+Measured on MI355X (p99 / worst top-minus-chosen / exact of 90): int8 + int8 KV
+0.037 / 0.016 / 88, int4 + fp8 KV 0.039 / 0.016 / 87, int4 0.023 / 0.016 / 87, OLMoE
+int4 experts + fp8 KV 0.19 / 0.016 / 86, OLMoE int8 + int8 KV 0.082 / 0.031 / 87, and FP8
+weight + activation 0.20 / 0.094 / 80: per-token e4m3 activations have 3 mantissa bits,
+so a 1-ulp bf16 difference upstream moves a code by 12.5% (the reference bounds native
+against emulated FP8 only by rel < 0.02, tests/test_quantizaton.py:75-88).
+The reference's own quantized-engine tests assert only non-empty output and fresh == cached
+tokens (test_models.py:152-187); the oracle comparison is stricter.
+"""
+import pytest
+import torch
+
+from oracle.runner import OracleKVCache, oracle_decode_attention, oracle_model
+
+PROMPTS = [[5, 9, 14, 3], [100, 200, 300, 400, 5, 6, 7, 8, 9, 10, 11, 12, 13], [42],
+           [7] * 8, [300, 2, 250, 11, 90], list(range(60, 80))]
+NEW_TOKENS = [12, 20, 7, 16, 25, 10]
+P99_TOL = {"fp8": 0.4, "olmoe": 0.3, "default": 0.08}
+NEAR_TIE = {"fp8": 0.2, "default": 0.05}
+
+
+def qwen3(dtype, seed=0, std=0.05):
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    torch.manual_seed(seed)
+    cfg = Qwen3Config(hidden_size=512, intermediate_size=1024, num_hidden_layers=2, num_attention_heads=4,
+                      num_key_value_heads=2, head_dim=128, vocab_size=512, max_position_embeddings=256,
+                      tie_word_embeddings=False, initializer_range=std, rope_theta=10000.0)
+    return Qwen3ForCausalLM(cfg).to(dtype).eval()
+
+
+def olmoe(dtype, seed=0, std=0.05):
+    from transformers import OlmoeConfig, OlmoeForCausalLM
+    torch.manual_seed(seed)
+    cfg = OlmoeConfig(hidden_size=512, intermediate_size=256, num_hidden_layers=2, num_attention_heads=4,
+                      num_key_value_heads=4, num_experts=8, num_experts_per_tok=2, vocab_size=512,
+                      max_position_embeddings=256, initializer_range=std, pad_token_id=1, eos_token_id=None,
+                      bos_token_id=None)
+    return OlmoeForCausalLM(cfg).to(dtype).eval()
+
+
+MODELS = {"qwen3": qwen3, "olmoe": olmoe}
+
+
+def cpu_runner(model, kv_dtype=None, pages=64, block=16):
+    from engine.core.model_runner import ModelRunner, PagePool
+    a = model.config
+    head_dim = getattr(a, "head_dim", None) or a.hidden_size // a.num_attention_heads
+    dtype = next(model.parameters()).dtype
+    cache = OracleKVCache(a.num_hidden_layers, a.num_key_value_heads, head_dim, pages * block, dtype, kv_dtype)
+    return ModelRunner(model, cache, decode_attention=oracle_decode_attention), PagePool(pages, block)
+
+
+def hf_greedy(model, prompt, n):
+    out = model.generate(torch.tensor([prompt]), max_new_tokens=n, do_sample=False, min_new_tokens=n,
+                         pad_token_id=1)
+    return out[0, len(prompt):].tolist()
+
+
+@pytest.mark.parametrize("name", ["qwen3", "olmoe"])
+def test_runner_matches_transformers_generate(name):
+    """The runner's glue (embeddings, RoPE, q/k norms, cache writes, prefill SDPA, decode
+    attention, MLP / MoE, head) reproduces transformers' greedy tokens exactly in fp32."""
+    from engine.core.model_runner import generate
+    model = MODELS[name](torch.float32)
+    runner, pool = cpu_runner(model)
+    got = generate(runner, pool, PROMPTS[:4], NEW_TOKENS[:4])
+    with torch.no_grad():
+        want = [hf_greedy(model, p, n) for p, n in zip(PROMPTS[:4], NEW_TOKENS[:4])]
+    assert got == want
+
+
+def test_oracle_cache_quantized_prefix_is_causal():
+    """Teacher forcing one prefill over a sequence gives the logits that token-by-token
+    decoding gives, also with an 8-bit cache (each token's codes depend on that token only):
+    the identity the GPU parity test relies on."""
+    from engine.core.model_runner import BatchMetadata, Request, generate
+    model = qwen3(torch.float32, seed=1)
+    runner, pool = cpu_runner(model, kv_dtype="int8")
+    logits = []
+    out = generate(runner, pool, [PROMPTS[1]], 6, logits_out=logits)[0]
+    runner2, pool2 = cpu_runner(model, kv_dtype="int8")
+    req = Request(0, PROMPTS[1] + out[:-1], 0)
+    pool2.ensure(req, len(req.all_ids))
+    meta = BatchMetadata([(req, 0, len(req.all_ids))], runner2.cache, pool2, "cpu")
+    full = runner2.forward(meta, all_logits=True)[len(PROMPTS[1]) - 1:]
+    assert torch.allclose(torch.stack(logits[0]), full, atol=1e-4, rtol=1e-4)
+
+
+# ------------------------------------------------------------------------ GPU
+GPU_CASES = [("qwen3", "int8_wo", "int8"), ("qwen3", "int4_wo", "fp8"), ("qwen3", "fp8", None),
+             ("qwen3", "int4_wo", None), ("olmoe", "int4_wo", "fp8"), ("olmoe", "int8_wo", "int8")]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,method,kv", GPU_CASES)
+def test_quantized_greedy_matches_oracle(name, method, kv):
+    from engine.core.kv_cache import KVCache
+    from engine.core.model_runner import BatchMetadata, ModelRunner, PagePool, Request, generate
+    from engine.quantization import get_method
+    from engine.quantization.loader import quantize_model
+    print(f"[case] greedy parity {name} {method} kv={kv}", flush=True)
+    dev = torch.device("cuda")
+    model = MODELS[name](torch.bfloat16)
+    m = get_method(method, device="cuda", compute_dtype=torch.bfloat16, group_size=128)
+    stats = quantize_model(model, m, ["experts", "linear"], "cuda")
+    assert stats["linear"] > 0 and (name != "olmoe" or stats["experts"] == 2)
+    cfg = model.config
+    pages, block = 64, 16
+    cache = KVCache("paged", cfg.num_hidden_layers, cfg.num_key_value_heads, 128, pages * block, torch.bfloat16, dev,
+                    block_size=block, kv_dtype=kv)
+    runner = ModelRunner(model, cache)
+    logits = []
+    outs = generate(runner, PagePool(pages, block), PROMPTS, NEW_TOKENS, logits_out=logits)
+    assert [len(o) for o in outs] == NEW_TOKENS
+    # the same codes through the bf16 restatement, teacher-forced on the GPU's tokens
+    ref = oracle_model(model, torch.bfloat16)
+    p99_tol = P99_TOL["fp8"] if method == "fp8" else P99_TOL.get(name, P99_TOL["default"])
+    near = NEAR_TIE.get(method, NEAR_TIE["default"])
+    total = exact = 0
+    errs = []
+    for i, (prompt, out) in enumerate(zip(PROMPTS, outs)):
+        orunner, opool = cpu_runner(ref, kv_dtype=kv)
+        req = Request(0, prompt + out[:-1], 0)
+        opool.ensure(req, len(req.all_ids))
+        meta = BatchMetadata([(req, 0, len(req.all_ids))], orunner.cache, opool, "cpu")
+        want = orunner.forward(meta, all_logits=True)[len(prompt) - 1:].float()
+        got = torch.stack(logits[i])
+        errs.append((got - want).abs().flatten())
+        top = want.max(dim=-1).values
+        chosen = want[torch.arange(len(out)), torch.tensor(out)]
+        gap = (top - chosen).max().item()
+        assert gap <= near, f"prompt {i}: a token is {gap:.3f} below the oracle's greedy choice"
+        exact += int((want.argmax(dim=-1) == torch.tensor(out)).sum())
+        total += len(out)
+    p99 = torch.cat(errs).quantile(0.99).item()
+    print(f"  logit |error| p99 {p99:.4f}; tokens equal to the oracle's argmax: {exact}/{total}", flush=True)
+    assert p99 <= p99_tol
+    assert exact >= 0.85 * total
