@@ -375,10 +375,12 @@ paged_decode_split8_kernel(AttnParams p) {
   bf16x8 qf[4];
   {
     const bool real = r < GROUP;
-    const uint16_t* qp = p.q + (int64_t)b * p.qs_b + (int64_t)(kvh * GROUP + (real ? r : 0)) * p.qs_h + g * 32;
+    // MFMA j of lane (g, r) takes dims 16 g + 8 j (j < 2) and 64 + 16 g + 8 (j - 2): the
+    // order in which the K loads below deliver a token's 128 bytes
+    const uint16_t* qp = p.q + (int64_t)b * p.qs_b + (int64_t)(kvh * GROUP + (real ? r : 0)) * p.qs_h + g * 16;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      uint4 u = real ? *reinterpret_cast<const uint4*>(qp + j * 8) : make_uint4(0, 0, 0, 0);
+      uint4 u = real ? *reinterpret_cast<const uint4*>(qp + (j < 2 ? 8 * j : 64 + 8 * (j - 2))) : make_uint4(0, 0, 0, 0);
       qf[j] = bf16x8_from(u.x, u.y, u.z, u.w);
     }
   }
@@ -423,13 +425,23 @@ paged_decode_split8_kernel(AttnParams p) {
   };
 
   // ---- the pieces of one chunk of CS x 32 tokens starting at c0
+  // K of 16 tokens comes in two loads of 8 tokens x 128 bytes (whole cache lines): load h
+  // reads token 8 h + (r & 7), 16-byte chunk ((r >> 3) ^ h) * 4 + g; k_swizzle turns the
+  // pair into token r, chunks g and 4 + g for lane (g, r)
   typedef int KSlots[CS][2];
+  typedef int KLoadSlots[CS][2][2];
   typedef int VSlots[CS][4];
+  const int kchunk[2] = {((r >> 3) * 4 + g) * 16, (((r >> 3) ^ 1) * 4 + g) * 16};
+  KLoadSlots kls;
   auto lookup = [&](int c0, KSlots& ks, VSlots& vs) {  // K / P tokens c0 + 32 s + 16 c + r, V tokens c0 + 32 s + tq + i
 #pragma unroll
     for (int s = 0; s < CS; ++s) {
 #pragma unroll
-      for (int c = 0; c < 2; ++c) ks[s][c] = (int)slot_of(min(c0 + s * kStep + c * 16 + r, t_end - 1));
+      for (int c = 0; c < 2; ++c) {
+        ks[s][c] = (int)slot_of(min(c0 + s * kStep + c * 16 + r, t_end - 1));
+#pragma unroll
+        for (int h = 0; h < 2; ++h) kls[s][c][h] = (int)slot_of(min(c0 + s * kStep + c * 16 + 8 * h + (r & 7), t_end - 1));
+      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) vs[s][i] = (int)slot_of(min(c0 + s * kStep + tq + i, t_end - 1));
     }
@@ -442,9 +454,9 @@ paged_decode_split8_kernel(AttnParams p) {
     for (int s = 0; s < CS; ++s)
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const uint8_t* kp = p.k + (int64_t)ks[s][c] * p.kvs_t + head_off + g * 32;
-        kr[bi][s][c][0] = *reinterpret_cast<const uint4*>(kp);
-        kr[bi][s][c][1] = *reinterpret_cast<const uint4*>(kp + 16);
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          kr[bi][s][c][h] = *reinterpret_cast<const uint4*>(p.k + (int64_t)kls[s][c][h] * p.kvs_t + head_off + kchunk[h]);
         if (HAS_SCALE) ksr[bi][s][c] = load_sd_raw<SD>(p.ks, (int64_t)ks[s][c] * p.ss_t + (int64_t)kvh * p.ss_h);
       }
   };
@@ -460,6 +472,15 @@ paged_decode_split8_kernel(AttnParams p) {
       }
     }
   };
+  const bool lo_half = r < 8;
+  auto k_swizzle = [&](const uint4& i0, const uint4& i1, uint4& f0, uint4& f1) {
+    const uint4 a = lo_half ? i0 : i1, b2 = lo_half ? i1 : i0;
+    f0 = a;
+    f1.x = __builtin_amdgcn_update_dpp(0u, b2.x, 0x128, 0xf, 0xf, false);  // row_ror:8
+    f1.y = __builtin_amdgcn_update_dpp(0u, b2.y, 0x128, 0xf, 0xf, false);
+    f1.z = __builtin_amdgcn_update_dpp(0u, b2.z, 0x128, 0xf, 0xf, false);
+    f1.w = __builtin_amdgcn_update_dpp(0u, b2.w, 0x128, 0xf, 0xf, false);
+  };
   float sc[CS][2][4];
   // scores of the chunk (lane: heads 4 g + v of tokens c0 + 32 s + 16 c + r) and one
   // online-softmax update for all of them
@@ -470,10 +491,12 @@ paged_decode_split8_kernel(AttnParams p) {
       for (int c = 0; c < 2; ++c) {
         bf16x8 kf[4];
         uint32_t o[4];
-        bytes8_to_bf16<KVT>(kr[bi][s][c][0].x, kr[bi][s][c][0].y, o); kf[0] = bf16x8_from(o[0], o[1], o[2], o[3]);
-        bytes8_to_bf16<KVT>(kr[bi][s][c][0].z, kr[bi][s][c][0].w, o); kf[1] = bf16x8_from(o[0], o[1], o[2], o[3]);
-        bytes8_to_bf16<KVT>(kr[bi][s][c][1].x, kr[bi][s][c][1].y, o); kf[2] = bf16x8_from(o[0], o[1], o[2], o[3]);
-        bytes8_to_bf16<KVT>(kr[bi][s][c][1].z, kr[bi][s][c][1].w, o); kf[3] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        uint4 k0, k1;
+        k_swizzle(kr[bi][s][c][0], kr[bi][s][c][1], k0, k1);
+        bytes8_to_bf16<KVT>(k0.x, k0.y, o); kf[0] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        bytes8_to_bf16<KVT>(k0.z, k0.w, o); kf[1] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        bytes8_to_bf16<KVT>(k1.x, k1.y, o); kf[2] = bf16x8_from(o[0], o[1], o[2], o[3]);
+        bytes8_to_bf16<KVT>(k1.z, k1.w, o); kf[3] = bf16x8_from(o[0], o[1], o[2], o[3]);
         f32x4 s4 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int j = 0; j < 4; ++j) s4 = mfma16(qf[j], kf[j], s4);
@@ -699,10 +722,16 @@ void launch_split3(const AttnParams& p, dim3 grid, hipStream_t st) {
   if (KVT == MIQ_BF16) {
     hipLaunchKernelGGL((paged_decode_split_kernel<KVT, HS, SD>), grid, dim3(kWaves * 64), 0, st, p);
   } else {
-    // 512-token partitions (the benchmark's): 2 wavefronts x 4 chunks of 64 tokens
-    // each, pipelined; any other partition: 4 wavefronts, chunk after chunk
+    // 128 / 256 / 512-token partitions: 1 / 2 / 4 wavefronts of 2 chunks of 64 tokens,
+    // pipelined over two register sets (256, the default, measured fastest on MI355X; a
+    // 4-chunk pipeline needs more than 256 VGPRs); any other partition: 4 wavefronts,
+    // chunk after chunk
     if (p.partition == 512)
-      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 4, 2>), grid, dim3(2 * 64), 0, st, p);
+      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 4>), grid, dim3(4 * 64), 0, st, p);
+    else if (p.partition == 256)
+      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 2>), grid, dim3(2 * 64), 0, st, p);
+    else if (p.partition == 128)
+      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 1>), grid, dim3(1 * 64), 0, st, p);
     else
       hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 0, 4>), grid, dim3(4 * 64), 0, st, p);
   }

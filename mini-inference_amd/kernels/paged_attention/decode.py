@@ -4,7 +4,7 @@
 Differences in mechanism, not in results:
   * one workgroup handles all query heads of a kv head (the K/V bytes are read once);
   * the context of each request is cut into fixed partitions of `partition` tokens
-    (multiple of 128; 512 by default) instead of a per-request count of splits. Passing
+    (multiple of 128; 256 by default) instead of a per-request count of splits. Passing
     num_splits keeps the reference's meaning of "about that many pieces for the longest
     request": the partition becomes cdiv(max_len, num_splits) rounded up to 128.
 The workspace (per-partition outputs and log-sum-exps) comes from torch's allocator, so
@@ -17,7 +17,7 @@ import torch
 
 from kernels import _lib as L
 
-DEFAULT_PARTITION = 512
+DEFAULT_PARTITION = 256
 _KV_DTYPES = (torch.bfloat16, torch.float8_e4m3fn, torch.int8)
 
 

@@ -93,20 +93,24 @@ def test_partitions_agree():
 
 
 @pytest.mark.parametrize("kind", ["int8", "fp8"])
-def test_quantized_cache_written_by_kvcache(kind):
-    """reference tests/test_paged_attention.py:73-89 with the HIP quantize-on-write."""
+@pytest.mark.parametrize("partition,lens", [(None, [40, 7, 90]), (128, [600, 7, 1290, 300]),
+                                            (256, [600, 7, 1290, 300]), (384, [600, 7, 1290]),
+                                            (512, [600, 7, 1290, 1100])])
+def test_quantized_cache_written_by_kvcache(kind, partition, lens):
+    """reference tests/test_paged_attention.py:73-89 with the HIP quantize-on-write; every
+    partition size with its own kernel instance (128, 256, 512) and the generic one (384),
+    with requests that end inside a chunk, a partition, or after one token."""
     from engine.core.kv_cache import KVCache
-    case(f"quantized cache {kind}")
+    case(f"quantized cache {kind} partition {partition} lens {lens}")
     H = KV = 4
     D, page = 128, 16
-    lens = [40, 7, 90]
     q, k, v, t, sl = random_paged(lens, H, KV, D, page, seed=2)
     cache = KVCache("paged", 1, KV, D, k.shape[0] + 16, torch.bfloat16, DEV, block_size=page, kv_dtype=kind)
     cache.write(0, torch.arange(k.shape[0], device=DEV), k.to(DEV), v.to(DEV))
     kc, vc = cache.k[0][: k.shape[0]].cpu(), cache.v[0][: k.shape[0]].cpu()
     ks, vs = cache.k_scale[0][: k.shape[0]].cpu(), cache.v_scale[0][: k.shape[0]].cpu()
     want = A.paged_decode_reference(q, kc, vc, t, sl, page, D ** -0.5, k_scale=ks, v_scale=vs)
-    got = run(q, kc, vc, t, sl, page, D ** -0.5, k_scale=ks, v_scale=vs)
+    got = run(q, kc, vc, t, sl, page, D ** -0.5, k_scale=ks, v_scale=vs, partition=partition)
     full = A.paged_decode_reference(q, k, v, t, sl, page, D ** -0.5)
     assert rel_error(got, want) < TOL and rel_error(got, full) < 0.1
     within(got, want)
