@@ -350,7 +350,7 @@ paged_decode_split_kernel(AttnParams p) {
 //   * P goes to LDS through the hardware float -> bf16 conversion; V is dequantized,
 //     transposed in registers (byte permutes) and written to LDS per 32-token step;
 //     masking of V past the context is only done in the chunk that reaches it.
-template <int KVT, bool HAS_SCALE, int SD, int CS, int NC, int W>
+template <int KVT, bool HAS_SCALE, int SD, int CS, int NC, int W, bool P16 = false>
 __global__ void __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2)))
 paged_decode_split8_kernel(AttnParams p) {
   const int part = blockIdx.y, kvh = blockIdx.x, b = blockIdx.z;  // kv heads of one partition are dispatched together (they share DRAM pages)
@@ -410,7 +410,7 @@ paged_decode_split8_kernel(AttnParams p) {
   constexpr int kBtMax = NC > 0 ? W * NC * kChunk + 1 : 1;
   __shared__ int s_bt[kBtMax];
   const int pg0 = pshift >= 0 ? p0 >> pshift : p0 / page;
-  if (NC > 0) {
+  if (NC > 0 && !P16) {
     const int pg1 = (min(p0 + p.partition, L) - 1 + page) / page;  // one past the last page in use
     for (int i = tid; i < pg1 - pg0; i += W * 64) s_bt[i] = btrow[pg0 + i];
     __syncthreads();
@@ -424,6 +424,19 @@ paged_decode_split8_kernel(AttnParams p) {
     return (int64_t)btrow[t / page] * page + t % page;
   };
 
+  // P16 (16-token pages): every 16-token group of a chunk lies in one page, so the page ids
+  // are the same in every lane: the wavefront's pages are loaded once into scalar
+  // registers (no LDS staging, no barrier, no dependent vector load before the first K / V
+  // request). Pages past the request's last one are clamped to it (their tokens are masked).
+  constexpr int kPagesPerChunk = CS * kStep / 16;
+  constexpr int kWP = P16 ? NC * kPagesPerChunk : 1;
+  int wpage[kWP];
+  if constexpr (P16) {
+    const int wpg0 = t_begin >> 4, pg_last = (L - 1) >> 4;
+#pragma unroll
+    for (int j = 0; j < kWP; ++j) wpage[j] = btrow[min(wpg0 + j, pg_last)];
+  }
+
   // ---- the pieces of one chunk of CS x 32 tokens starting at c0
   // K of 16 tokens comes in two loads of 8 tokens x 128 bytes (whole cache lines): load h
   // reads token 8 h + (r & 7), 16-byte chunk ((r >> 3) ^ h) * 4 + g; k_swizzle turns the
@@ -433,7 +446,26 @@ paged_decode_split8_kernel(AttnParams p) {
   typedef int VSlots[CS][4];
   const int kchunk[2] = {((r >> 3) * 4 + g) * 16, (((r >> 3) ^ 1) * 4 + g) * 16};
   KLoadSlots kls;
-  auto lookup = [&](int c0, KSlots& ks, VSlots& vs) {  // K / P tokens c0 + 32 s + 16 c + r, V tokens c0 + 32 s + tq + i
+  // chunk ci of the wavefront starts at token c0 (ci is a compile-time index where P16 uses it)
+  auto lookup = [&](int c0, int ci, KSlots& ks, VSlots& vs) {  // K / P tokens c0 + 32 s + 16 c + r, V tokens c0 + 32 s + tq + i
+    if constexpr (P16) {
+#pragma unroll
+      for (int s = 0; s < CS; ++s) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const int pg = wpage[ci * kPagesPerChunk + 2 * s + c];
+          ks[s][c] = pg * 16 + r;
+#pragma unroll
+          for (int h = 0; h < 2; ++h) kls[s][c][h] = pg * 16 + 8 * h + (r & 7);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tt = tq + i;
+          vs[s][i] = (tt < 16 ? wpage[ci * kPagesPerChunk + 2 * s] : wpage[ci * kPagesPerChunk + 2 * s + 1]) * 16 + (tt & 15);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int s = 0; s < CS; ++s) {
 #pragma unroll
@@ -586,7 +618,7 @@ paged_decode_split8_kernel(AttnParams p) {
     for (int c0 = t_begin; c0 < t_end; c0 += kChunk) {
       KSlots ks;
       VSlots vs;
-      lookup(c0, ks, vs);
+      lookup(c0, 0, ks, vs);
       issue_k(0, ks);
       issue_v(0, ks, vs);
       scores(0, c0);
@@ -603,7 +635,7 @@ paged_decode_split8_kernel(AttnParams p) {
       for (int c = 0; c < NB; ++c) {
         const int c0 = t_begin + c * kChunk;
         if (c == 0 || c0 < t_end) {
-          lookup(c0, ks, vs);
+          lookup(c0, c, ks, vs);
           issue_k(c, ks);
           issue_v(c, ks, vs);
         }
@@ -618,7 +650,7 @@ paged_decode_split8_kernel(AttnParams p) {
           if (c == 0) MIQ_TRACE(2);
           pv(bi, c0);
           if (c + NB < NC && c0 + NB * kChunk < t_end) {
-            lookup(c0 + NB * kChunk, ks, vs);
+            lookup(c0 + NB * kChunk, c + NB, ks, vs);
             issue_k(bi, ks);
             issue_v(bi, ks, vs);
           }
@@ -726,10 +758,18 @@ void launch_split3(const AttnParams& p, dim3 grid, hipStream_t st) {
     // pipelined over two register sets (256, the default, measured fastest on MI355X; a
     // 4-chunk pipeline needs more than 256 VGPRs); any other partition: 4 wavefronts,
     // chunk after chunk
-    if (p.partition == 512)
+    // 16-token pages (the reference's block size) take the scalar page-id path
+    const bool p16 = p.page == 16;
+    if (p.partition == 512 && p16)
+      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 4, true>), grid, dim3(4 * 64), 0, st, p);
+    else if (p.partition == 512)
       hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 4>), grid, dim3(4 * 64), 0, st, p);
+    else if (p.partition == 256 && p16)
+      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 2, true>), grid, dim3(2 * 64), 0, st, p);
     else if (p.partition == 256)
       hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 2>), grid, dim3(2 * 64), 0, st, p);
+    else if (p.partition == 128 && p16)
+      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 1, true>), grid, dim3(1 * 64), 0, st, p);
     else if (p.partition == 128)
       hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 1>), grid, dim3(1 * 64), 0, st, p);
     else
