@@ -13,6 +13,8 @@
 // with the same (lane / 16) * 32 byte offset along k, so whatever order the hardware
 // assigns to those 32 bytes inside the instruction, A and B agree and the sum over k is
 // the dot product.
+#include <cstdlib>
+
 #include "miq_common.h"
 
 namespace miq {
@@ -174,6 +176,194 @@ int launch(const uint8_t* xq, const float* xs, const uint8_t* wq, const float* w
   return check_launch("fp8_gemm");
 }
 
+
+// ---------------------------------------------------------------- 32x32 MFMA kernel
+// The large-tile kernel: a 256 x 192 tile per workgroup (one per CU at the prefill shape),
+// 4 wavefronts of 128 x 96 each on v_mfma_scale_f32_32x32x64_f8f6f4 (12 accumulator
+// tiles of 32 x 32 = 192 fp32 per lane, in AGPRs).
+//
+// Operands go from HBM straight to LDS (buffer_load_dwordx4 ... lds: no registers, no
+// LDS store instructions) through a ring of NS stages of 64 k; stage s + NS - 1 is
+// requested while stage s is multiplied, so NS - 1 stages of load latency are hidden.
+// A stage is 256 + 192 rows of 64 bytes; each wavefront issues 7 of its 28 one-KiB
+// loads. One wait on the wavefront's own loads and one barrier per stage.
+//
+// LDS row layout: the 4 chunks of 16 bytes of row R sit at positions c ^ ((R >> 2) & 3),
+// so the 16 rows that 16 lanes read for one fragment hit 16 different 4-bank groups. A
+// load writes 64 lanes x 16 bytes contiguously, so each lane fetches the global chunk
+// that belongs at its position.
+//
+// Fragments: for the 32x32x64 MFMA, lane l supplies 32 bytes of row l % 32 of A (and of
+// column l % 32 of B) at k offset (l / 32) * 32; A and B use the same offsets, so the
+// instruction's internal byte order cannot change the dot product. Accumulator element i
+// of lane l is C[row (i / 4) * 8 + (l / 32) * 4 + i % 4][col l % 32].
+constexpr int BK32 = 64;                 // k per stage
+constexpr int kStages32 = 5;             // ring depth
+
+__device__ inline f32x16 mfma32_fp8(i32x8 a, i32x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+template <int N>
+__device__ inline void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int BM, int BN>
+__global__ void __launch_bounds__(256)
+fp8_gemm32_kernel(const uint8_t* __restrict__ A, const float* __restrict__ sa,
+                  const uint8_t* __restrict__ B, const float* __restrict__ sb,
+                  uint16_t* __restrict__ Y, int64_t ldy, int M, int N, int K, int tiles_m,
+                  int tiles_n, int xcd_panels) {
+  constexpr int kThreads = 256, WM = 2, WN = 2, NS = kStages32;
+  constexpr int kWaveM = BM / WM, kWaveN = BN / WN;    // 128 x 96
+  constexpr int kTM = kWaveM / 32, kTN = kWaveN / 32;  // 4 x 3 tiles of 32 x 32
+  constexpr int kRowBytes = BK32;                      // 64
+  constexpr int kStage = (BM + BN) * kRowBytes;        // 28 KiB
+  constexpr int kLoadsA = BM / 16, kLoadsB = BN / 16;  // 1-KiB loads (16 rows) per stage
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wv / WN, wn = wv - wm * WN;
+
+  int tm, tn;
+  const int bid = blockIdx.x;
+  if (xcd_panels) {  // each XCD walks all row tiles of its band of column tiles (B stays in its L2)
+    const int xcd = bid & 7, local = bid >> 3;
+    tm = local % tiles_m;
+    tn = xcd * (tiles_n / 8) + local / tiles_m;
+  } else {
+    tm = bid % tiles_m;
+    tn = bid / tiles_m;
+  }
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  // this lane's part of every load: row lane / 4 of the 16, global chunk (lane & 3) ^
+  // ((lane >> 4) & 3); rows past M or N read zeros (the descriptor's size)
+  const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(A), 0, M * K, 0x00020000);
+  const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(B), 0, N * K, 0x00020000);
+  const int lrow = lane >> 2, lchunk = (lane & 3) ^ ((lane >> 4) & 3);
+  const int voffA = (m0 + lrow) * K + lchunk * 16, voffB = (n0 + lrow) * K + lchunk * 16;
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  // wavefront w issues A loads 4 w .. 4 w + 3 (rows 64 w ..) and B loads 3 w .. 3 w + 2
+  // (rows 48 w ..) of each stage: the operand of every load is known at compile time
+  static_assert(kLoadsA == 16 && kLoadsB == 12, "load split assumes a 256 x 192 tile");
+  const int qa0 = wv * 4, qb0 = wv * 3;
+  auto issue = [&](int st, int slot) {  // stage st into ring slot `slot`
+    uint8_t* base = smem + slot * kStage;
+    const int k0 = st * BK32;
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ars, (lds_ptr)(base + (qa0 + u) * 1024), 16, voffA + k0,
+                                               (qa0 + u) * 16 * K, 0, 0);
+#pragma unroll
+    for (int u = 0; u < 3; ++u)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(brs, (lds_ptr)(base + BM * kRowBytes + (qb0 + u) * 1024), 16,
+                                               voffB + k0, (qb0 + u) * 16 * K, 0, 0);
+  };
+
+  f32x16 acc[kTM][kTN];
+#pragma unroll
+  for (int i = 0; i < kTM; ++i)
+#pragma unroll
+    for (int j = 0; j < kTN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // fragment of rows row0 + (lane % 32) (row0 a multiple of 32): chunks 2 (lane / 32) and
+  // + 1, at positions that depend on the lane only
+  const int fr = lane & 31, fq = lane >> 5;
+  const int fsw = (fr >> 2) & 3;
+  const int foff0 = fr * kRowBytes + (((fq * 2) ^ fsw) << 4), foff1 = fr * kRowBytes + (((fq * 2 + 1) ^ fsw) << 4);
+  auto frag = [&](const uint8_t* buf, int row0) -> i32x8 {
+    const i32x4 lo = *reinterpret_cast<const i32x4*>(buf + row0 * kRowBytes + foff0);
+    const i32x4 hi = *reinterpret_cast<const i32x4*>(buf + row0 * kRowBytes + foff1);
+    return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
+
+  const int nsteps = K / BK32;
+#pragma unroll
+  for (int st = 0; st < NS - 1; ++st)
+    if (st < nsteps) issue(st, st);
+  int slot = 0, next_slot = NS - 1;  // ring slots of stage s and of stage s + NS - 1
+  for (int s = 0; s < nsteps; ++s) {
+    // this wavefront's loads of stage s are done once at most (NS - 2) stages of loads
+    // issued after it remain; then every wavefront's (barrier), and the slot of stage
+    // s - 1 is free for stage s + NS - 1
+    if (s + NS - 2 < nsteps) wait_vmcnt<(kStages32 - 2) * ((BM / 16 + BN / 16) / 4)>();
+    else wait_vmcnt<0>();
+    // a bare barrier: __syncthreads() would also wait for every load in flight (the later
+    // stages too); the fragment reads of stage s - 1 have completed (their MFMAs waited)
+    asm volatile("s_barrier" ::: "memory");
+    if (s + NS - 1 < nsteps) issue(s + NS - 1, next_slot);
+    const uint8_t* cur = smem + slot * kStage;
+    slot = slot == NS - 1 ? 0 : slot + 1;
+    next_slot = next_slot == NS - 1 ? 0 : next_slot + 1;
+    i32x8 bf[kTN];
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) bf[j] = frag(cur + BM * kRowBytes, wn * kWaveN + j * 32);
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+      const i32x8 af = frag(cur, wm * kWaveM + i * 32);
+#pragma unroll
+      for (int j = 0; j < kTN; ++j) acc[i][j] = mfma32_fp8(af, bf[j], acc[i][j]);
+    }
+  }
+
+  // epilogue: y = bf16(acc * sa[m] * sb[n]). The wavefront's 128 x 96 bf16 tile goes through LDS (the
+  // ring is free once every wavefront is past its last stage) and out as 16-byte row
+  // pieces, instead of 192 scattered 2-byte stores per lane.
+  const int mw = m0 + wm * kWaveM, nw = n0 + wn * kWaveN;
+  float wsn[kTN];
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) wsn[j] = sb[min(nw + j * 32 + fr, N - 1)];
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  constexpr int kCRow = kWaveN + 8;  // bf16 per LDS row of the wavefront's tile
+  uint16_t* ct = reinterpret_cast<uint16_t*>(smem) + wv * (kWaveM * kCRow);
+#pragma unroll
+  for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) {
+      const int r0 = i * 32 + e4 * 8 + fq * 4;  // rows r0 .. r0 + 3 of the wavefront tile
+      float xsv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xsv[e] = sa[min(mw + r0 + e, M - 1)];
+#pragma unroll
+      for (int j = 0; j < kTN; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          ct[(r0 + e) * kCRow + j * 32 + fr] = f32_to_bf16(acc[i][j][e4 * 4 + e] * xsv[e] * wsn[j]);
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  constexpr int kPiecesRow = kWaveN / 8;                  // 16-byte pieces per row: 12
+  constexpr int kPieces = kWaveM * kPiecesRow / 64;       // per lane: 24
+#pragma unroll
+  for (int u = 0; u < kPieces; ++u) {
+    const int pc = lane + u * 64, row = pc / kPiecesRow, col = (pc - row * kPiecesRow) * 8;
+    const int m = mw + row, n = nw + col;
+    const uint4 v = *reinterpret_cast<const uint4*>(ct + row * kCRow + col);
+    if (m < M && n < N) *reinterpret_cast<uint4*>(Y + (int64_t)m * ldy + n) = v;
+  }
+}
+
+template <int BM, int BN>
+int launch32(const uint8_t* xq, const float* xs, const uint8_t* wq, const float* ws, uint16_t* y,
+             int64_t ldy, int M, int N, int K, hipStream_t st) {
+  const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  const int xcd = (tn % 8 == 0) ? 1 : 0;
+  constexpr size_t kLds = (size_t)kStages32 * (BM + BN) * BK32;
+  static bool attr_set = false;
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fp8_gemm32_kernel<BM, BN>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((fp8_gemm32_kernel<BM, BN>), dim3((unsigned)(tm * tn)), dim3(256), kLds, st, xq, xs, wq, ws,
+                     y, ldy, M, N, K, tm, tn, xcd);
+  return check_launch("fp8_gemm");
+}
+
 }  // namespace
 }  // namespace miq
 
@@ -190,7 +380,13 @@ extern "C" int miq_fp8_gemm(const uint8_t* xq, const float* x_scale, const uint8
               "fp8_gemm: operands must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   uint16_t* yy = static_cast<uint16_t*>(y);
-  if (M >= 1024 && N % 192 == 0)
+  if (M >= 1024 && N % 192 == 0) {
+    // the large-tile kernel addresses the operands through buffer descriptors (< 2 GiB)
+    // and stores 16-byte pieces of y rows
+    if (!getenv("MIQ_FP8_OLD") && M * K < 0x7fffffffLL && N * K < 0x7fffffffLL && ldy % 8 == 0 &&
+        (reinterpret_cast<uintptr_t>(y) & 15) == 0)
+      return launch32<256, 192>(xq, x_scale, wq, w_scale, yy, ldy, (int)M, (int)N, (int)K, st);
     return launch<256, 192, 4, 2>(xq, x_scale, wq, w_scale, yy, ldy, (int)M, (int)N, (int)K, st);
+  }
   return launch<128, 128, 2, 2>(xq, x_scale, wq, w_scale, yy, ldy, (int)M, (int)N, (int)K, st);
 }
