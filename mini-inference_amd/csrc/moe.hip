@@ -259,6 +259,10 @@ moe_down_kernel(MoeParams p, int chunk_steps) {
 enum { MOE_GU = 0, MOE_DN = 1 };
 constexpr int kMoeD = 8;       // ring depth (k-steps; 16 measured slower)
 constexpr int kMoeChunk = 16;  // k-steps of activations staged at once
+#ifndef MIQ_MOE_RUN
+#define MIQ_MOE_RUN 2
+#endif
+constexpr int kItemsPerRun = MIQ_MOE_RUN;  // consecutive items per workgroup (one staging)
 
 template <int MODE, bool HZ, int SD>
 __global__ void __launch_bounds__(256)
@@ -292,9 +296,16 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
   int nsteps_v = steps;
   asm volatile("" : "+v"(nsteps_v));
 
-  for (int item = blockIdx.x;; item += gridDim.x) {
+  // a workgroup takes runs of kItemsPerRun consecutive items: they share a tile, so when
+  // the whole K fits one chunk its activations are staged once per run
+  const bool one_chunk = steps <= kMoeChunk;
+  int staged_tile = -1;
+  for (int k = 0;; ++k) {
+    const int item = (blockIdx.x + (k / kItemsPerRun) * gridDim.x) * kItemsPerRun + k % kItemsPerRun;
     const int tile = item / blocks_per_tile, blk = item - tile * blocks_per_tile;
     if (tile * kTile >= npad) break;
+    const bool stage = !(one_chunk && tile == staged_tile);
+    staged_tile = tile;
     const int e = p.expert_ids[tile];
     // weight rows of this wavefront's two tiles (within the whole [E * rows] matrix)
     int row[NR];
@@ -340,7 +351,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
         zq[d][t] = HZ ? __builtin_amdgcn_raw_buffer_load_b32(zrs, so, 0, 0) : 0u;
       }
     };
-    if (tid < kTile) {
+    if (stage && tid < kTile) {
       const int pair = p.sorted_ids[tile * kTile + tid];
       s_src[tid] = pair < p.num_pairs ? (MODE == MOE_GU ? pair / p.topk : tile * kTile + tid) : -1;
     }
@@ -369,7 +380,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
       const int xcols = nst * (kStepK / 8);
       const int npieces = kTile * xcols;
       if (c0) __syncthreads();
-      for (int base = 0; base < npieces; base += 4 * 256) {
+      for (int base = 0; base < (stage ? npieces : 0); base += 4 * 256) {
         uint4 xr[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -477,8 +488,9 @@ void launch_stream_experts(const MoeParams& p, int max_tiles, hipStream_t st) {
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_gu);
     attr = true;
   }
-  // about two workgroups per CU, never more than the items that could exist
-  const int grid_gu = std::min(512, max_tiles * bgu), grid_dn = std::min(512, max_tiles * bdn);
+  // about two workgroups per CU, never more than the runs of items that could exist
+  const int grid_gu = std::max(1, std::min(512, max_tiles * bgu / kItemsPerRun));
+  const int grid_dn = std::max(1, std::min(512, max_tiles * bdn / kItemsPerRun));
   hipLaunchKernelGGL((moe_stream_kernel<MOE_GU, HZ, SD>), dim3(grid_gu), dim3(256), lds_gu, st, p, bgu);
   hipLaunchKernelGGL((moe_stream_kernel<MOE_DN, HZ, SD>), dim3(grid_dn), dim3(256), lds_gu, st, p, bdn);
 }
