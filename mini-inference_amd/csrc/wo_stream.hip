@@ -185,6 +185,8 @@ wo_stream_kernel(StreamParams p) {
   const int xstride = CS * kStepK + 8;
   float* xsum = reinterpret_cast<float*>(lds + M * xstride);
   const int xld = (int)(p.ldx / 8);
+  const __amdgpu_buffer_rsrc_t xrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.x), 0, (int)((int64_t)M * p.ldx * 2), 0x00020000);
   // activation pieces (16 bytes) of chunk c0, round `base`: XP per thread; pieces j of a
   // round that no thread needs are not loaded (a uniform branch)
   uint4 xr[XP];
@@ -238,7 +240,37 @@ wo_stream_kernel(StreamParams p) {
     const int xcols = nst * (kStepK / 8);  // 16-byte pieces per activation row
     const int npieces = M * xcols;
     if (c0 != st0) __syncthreads();  // every wavefront is done with the previous chunk
-    for (int base = 0; base < npieces; base += XP * kThreads) {
+    if constexpr (KIND == KIND_INT8 && MT >= 2) {
+      // Several activation tiles (int8): the chunk's rows go from memory straight into their LDS
+      // rows (buffer_load ... lds, one round trip for the whole chunk: staging through
+      // registers took one round trip per 16 KiB), and one LDS pass forms the per-k-step
+      // sums. For int4 the register path measured the same (its activations are permuted
+      // to the unpack order on the way).
+      const int ipr = (xcols + 63) / 64;  // loads of up to 64 pieces per row
+      const int nload = M * ipr;
+      for (int q = wv; q < nload; q += kWaves) {
+        const int m = q / ipr, p0 = (q - m * ipr) * 64;
+        if (p0 + lane < xcols)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              xrs, (__attribute__((address_space(3))) void*)(lds + m * xstride + p0 * 8), 16,
+              (m * (int)p.ldx + c0 * kStepK + (p0 + lane) * 8) * 2, 0, 0, 0);
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      for (int i0 = 0; i0 < npieces; i0 += kThreads) {
+        const int i = i0 + tid;
+        const int ic = min(i, npieces - 1);
+        const int m = ic / xcols, c = ic - m * xcols;
+        const uint4 v = *reinterpret_cast<const uint4*>(lds + m * xstride + c * 8);
+        float sm = sum8_bf16(v);
+        sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x111, 0xf, 0xf, true));
+        sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x112, 0xf, 0xf, true));
+        sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x114, 0xf, 0xf, true));
+        sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x118, 0xf, 0xf, true));
+        if (i < npieces && (c & 15) == 15) xsum[(c >> 4) * XR + m] = sm;
+      }
+    }
+    for (int base = 0; base < (KIND == KIND_INT8 && MT >= 2 ? 0 : npieces); base += XP * kThreads) {
       if (MT > 1 || c0 != st0 || base != 0) load_x(c0, base);
 #pragma unroll
       for (int j = 0; j < XP; ++j) {
