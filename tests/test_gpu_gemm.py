@@ -89,9 +89,16 @@ INT4_SHAPES = [(1, 64, 256, 128), (5, 128, 512, 128), (8, 64, 1024, 256), (16, 1
 
 @pytest.mark.parametrize("M,N,K,group", INT4_SHAPES)
 @pytest.mark.parametrize("symmetric", [False, True])
-def test_w4a16_gemm(M, N, K, group, symmetric):
+@pytest.mark.parametrize("msplit", [None, "4,3", "0,0"])
+def test_w4a16_gemm(M, N, K, group, symmetric, msplit, monkeypatch):
+    """msplit: the default plan, the M split forced with 4 weight tiles per wavefront and
+    3 splits (one activation tile per workgroup), and the M split turned off."""
     from kernels import quant_ops as ops
-    case(f"w4a16 M={M} N={N} K={K} g={group} sym={symmetric}")
+    if msplit is not None:
+        if M <= 16:
+            pytest.skip("the M split applies to more than 16 rows")
+        monkeypatch.setenv("MIQ_WO_MSPLIT", msplit)
+    case(f"w4a16 M={M} N={N} K={K} g={group} sym={symmetric} msplit={msplit}")
     w = make_w(N, K, 20)
     x = make_x(M, K, 21)
     q = O.int4_quantize_symmetric(w, group) if symmetric else O.int4_quantize(w, group)
