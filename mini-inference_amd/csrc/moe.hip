@@ -319,14 +319,16 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
       row[1] = e * rows_per_expert + n0 + 16 + r;
     }
     // weight loads read whole 128-byte lines: load h of tile t covers its rows 8h .. 8h + 7
-    // over two k-steps; lane (g, r) reads row 8 h + (r & 7), chunk ((r >> 3) ^ h) * 4 + g
-    // (the raw loads of k-steps d, d + 1 sit in wq[d], wq[d + 1]; swizzled when used)
-    const int ch[2] = {(r >> 3) * 4 + g, ((r >> 3) ^ 1) * 4 + g};
+    // over two k-steps, in address order within each 64-byte half (lane 32 c2 + 4 rr + cl:
+    // row 8h + rr, bytes 64 c2 + 16 cl); the raw loads of k-steps d, d + 1 sit in wq[d],
+    // wq[d + 1] and lanes_to_mfma() gives the MFMA layout when they are used
+    const int lrr = (lane >> 2) & 7, lcl = lane & 3, lc2 = lane >> 5;
+    const int bp_addr = (32 * (r >> 3) + 4 * (r & 7) + g) * 4;
     int woff[NR][2], soff[NR];
 #pragma unroll
     for (int t = 0; t < NR; ++t) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) woff[t][h] = (int)((row[t] - r + 8 * h + (r & 7)) * ldw) + ch[h] * 16;
+      for (int h = 0; h < 2; ++h) woff[t][h] = (int)((row[t] - r + 8 * h + lrr) * ldw) + lc2 * 64 + lcl * 16;
       soff[t] = (int)(row[t] * ngroups);
     }
     uint4 wq[D][NR][NL];
@@ -339,7 +341,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
         if ((d & 1) == 0) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
-            const int kp = (kl + (ch[h] >> 2) - nsteps_v) >> 31;  // chunks 4..7: k-step kl + 1
+            const int kp = (kl + lc2 - nsteps_v) >> 31;  // second halves: k-step kl + 1
             const int off = ((woff[t][h] + kl * 64) & kp) | (kOut & ~kp);
             const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2 /* nt */);
             wq[d + h][t][0] = *reinterpret_cast<const uint4*>(&v);
@@ -359,15 +361,6 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
     for (int d = 0; d < D; ++d) request(d, d);
     __syncthreads();  // s_src ready (and the previous item is done with LDS)
 
-    const bool lo_half = r < 8;
-    auto swizzle = [&](const uint4& i0, const uint4& i1, uint4& f0, uint4& f1) {
-      const uint4 a = lo_half ? i0 : i1, b = lo_half ? i1 : i0;
-      f0 = a;
-      f1.x = __builtin_amdgcn_update_dpp(0u, b.x, 0x128, 0xf, 0xf, false);  // row_ror:8
-      f1.y = __builtin_amdgcn_update_dpp(0u, b.y, 0x128, 0xf, 0xf, false);
-      f1.z = __builtin_amdgcn_update_dpp(0u, b.z, 0x128, 0xf, 0xf, false);
-      f1.w = __builtin_amdgcn_update_dpp(0u, b.w, 0x128, 0xf, 0xf, false);
-    };
     uint4 wnext[NR];
     f32x4 acc[NR], accg[NR], xsg;
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
@@ -422,7 +415,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
             for (int t = 0; t < NR; ++t) {
               bf16x8 bv[4];
               uint4 wl;
-              if ((d & 1) == 0) swizzle(wq[d][t][0], wq[d + 1][t][0], wl, wnext[t]);
+              if ((d & 1) == 0) lanes_to_mfma(bp_addr, wq[d][t][0], wq[d + 1][t][0], wl, wnext[t]);
               else wl = wnext[t];
               unpack_b<KIND_INT4>(&wl, bv);
 #pragma unroll

@@ -10,7 +10,11 @@
 // instead of a ring of them. The activations (all of K) are staged in LDS once per
 // workgroup; the W partial tiles are added through LDS in wavefront order, so there is
 // no split-K workspace, no cross-workgroup counter and no second round trip for partial
-// sums. A launch has N / 16 workgroups of 4 to 16 wavefronts.
+// sums. A tile holds R <= 16 weight rows (the MFMA tile's other rows read nothing and
+// are not written): a launch has N / R workgroups of 4 to 16 wavefronts, R chosen so that
+// the workgroups cover every CU. One CU streams at a limited rate whatever the load on the
+// rest of the chip (on MI355X an M=1 tile of 16 x 9728 int4 weights takes as long with 80
+// workgroups in the launch as with 256), so the bytes per CU set the time.
 //
 // Per-element math is the one of the streamed kernel (wo_stream.hip): codes unpack to
 // bf16 128 + code, MFMA 16x16x32 bf16 with fp32 accumulation in two chains, per-group
@@ -18,8 +22,11 @@
 // codes) and acc - 128 * sum(x) then the row scale for int8.
 //
 // Weight loads read whole 128-byte lines: load h of the tile covers its rows 8h .. 8h + 7,
-// 128 bytes each (two int4 k-steps or one int8 k-step); a DPP row rotation then gives
-// every lane (g, r) row r, chunk g of each 64-byte half, the MFMA B layout.
+// 128 bytes each (two int4 k-steps or one int8 k-step), with four consecutive lanes on 64
+// contiguous bytes (an order with four rows per four lanes measured 60 % slower from L2
+// and 15 % slower from HBM on MI355X in a load-only test). A 32-lane swap and one lane
+// gather per dword (lanes_to_mfma) then give every lane (g, r) row r, chunk g of each
+// 64-byte half, the MFMA B layout.
 #include <algorithm>
 #include <cstdlib>
 
@@ -34,6 +41,7 @@ namespace miq {
 namespace {
 
 using namespace wo;
+
 
 constexpr int kTileNS = 8;                 // k-steps in flight per wavefront (all of its slice)
 constexpr int kTileLds = 160 * 1024;       // gfx950 LDS per workgroup
@@ -54,6 +62,7 @@ struct TileParams {
   uint16_t* y;
   int64_t ldy;
   int M, N, steps;      // steps = K / 128
+  int rows;             // weight rows per tile (1..16)
   int units, unit_steps;
   int wbytes, sbytes;
 };
@@ -96,13 +105,18 @@ wo_tile_kernel(TileParams p) {
   MIQ_TRACE(5);
 
   // ---- then every weight and scale word of the slice
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * p.rows;
   const int nrow = n0 + r;
-  const int ch[2] = {(r >> 3) * 4 + g, ((r >> 3) ^ 1) * 4 + g};
-  int woff[2];
+  const int nrows = min(p.rows, p.N - n0);  // rows of this tile that exist
+  // load h: lane 32 c2 + 4 rr + cl reads row 8h + rr, bytes 64 c2 + 16 cl of the k-step pair
+  const int lrr = (lane >> 2) & 7, lcl = lane & 3, lc2 = lane >> 5;
+  int woff[2], wok[2];
 #pragma unroll
-  for (int h = 0; h < 2; ++h)
-    woff[h] = min(n0 + 8 * h + (r & 7), p.N - 1) * (int)p.ldw + st0 * kStepBytes + ch[h] * 16;
+  for (int h = 0; h < 2; ++h) {
+    woff[h] = min(n0 + 8 * h + lrr, p.N - 1) * (int)p.ldw + st0 * kStepBytes + lc2 * 64 + lcl * 16;
+    wok[h] = (8 * h + lrr - nrows) >> 31;  // all ones for a row of the tile
+  }
+  const int bp_addr = (32 * (r >> 3) + 4 * (r & 7) + g) * 4;
   const int soff = (int)(min(nrow, p.N - 1) * p.ngroups + st0 / p.group_steps);
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.w), 0, p.wbytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.scale), 0, p.sbytes, 0x00020000);
@@ -121,7 +135,7 @@ wo_tile_kernel(TileParams p) {
     if (KIND == KIND_INT8 || (d & 1) == 0) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int kp = (d + (KIND == KIND_INT4 ? (ch[h] >> 2) : 0) - nsteps_v) >> 31;
+        const int kp = ((d + (KIND == KIND_INT4 ? lc2 : 0) - nsteps_v) >> 31) & wok[h];
         const int off = ((woff[h] + d * kStepBytes) & kp) | (kOut & ~kp);
         const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2 /* nt */);
         if (KIND == KIND_INT4) wq[d + h][0] = *reinterpret_cast<const uint4*>(&v);
@@ -133,7 +147,7 @@ wo_tile_kernel(TileParams p) {
   // 16-byte loads from the aligned word holding the first one
   constexpr int esz = SD == MIQ_F32 ? 4 : 2;
   uint32_t sw[8], zw[8];
-  const int sbase = (soff * esz) & ~3;
+  const int sbase = r < nrows ? (soff * esz) & ~3 : kOut - 32;
   if (KIND == KIND_INT4) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -187,15 +201,6 @@ wo_tile_kernel(TileParams p) {
   MIQ_TRACE(2);
 
   // ---- multiply the slice
-  const bool lo_half = r < 8;
-  auto swizzle = [&](const uint4& i0, const uint4& i1, uint4& f0, uint4& f1) {
-    const uint4 a = lo_half ? i0 : i1, b = lo_half ? i1 : i0;
-    f0 = a;
-    f1.x = __builtin_amdgcn_update_dpp(0u, b.x, 0x128, 0xf, 0xf, false);
-    f1.y = __builtin_amdgcn_update_dpp(0u, b.y, 0x128, 0xf, 0xf, false);
-    f1.z = __builtin_amdgcn_update_dpp(0u, b.z, 0x128, 0xf, 0xf, false);
-    f1.w = __builtin_amdgcn_update_dpp(0u, b.w, 0x128, 0xf, 0xf, false);
-  };
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
   f32x4 acc = z4, accg = z4, acc2 = z4, xsg = z4;
   int c_grp = 0, c_left = p.group_steps;
@@ -214,9 +219,9 @@ wo_tile_kernel(TileParams p) {
       xsg += *reinterpret_cast<const f32x4*>(xsum + kl * 16 + g * 4);
       uint4 wl[2];
       if (KIND == KIND_INT8) {
-        swizzle(wq[d][0], wq[d][1], wl[0], wl[1]);
+        lanes_to_mfma(bp_addr, wq[d][0], wq[d][1], wl[0], wl[1]);
       } else if ((d & 1) == 0) {
-        swizzle(wq[d][0], wq[d + 1][0], wl[0], wnext);
+        lanes_to_mfma(bp_addr, wq[d][0], wq[d + 1][0], wl[0], wnext);
       } else {
         wl[0] = wnext;
       }
@@ -272,7 +277,7 @@ wo_tile_kernel(TileParams p) {
   __syncthreads();
   for (int t = tid; t < M * 16; t += kThreads) {
     const int m = t >> 4, n = n0 + (t & 15);
-    if (n >= p.N) continue;
+    if ((t & 15) >= nrows) continue;
     float o = 0.f;
 #pragma unroll
     for (int w = 0; w < W; ++w) o += red[w * M * 16 + t];
@@ -314,12 +319,12 @@ void launch_tile_sd(int sd, int W, const TileParams& p, unsigned blocks, size_t 
 // apply: more than 16 rows, a slice longer than 8 k-steps, or activations too large for
 // LDS), the unit of K slicing and the LDS bytes.
 struct TilePlan {
-  int W, units, unit_steps;
+  int W, units, unit_steps, rows;
   size_t lds_bytes;
 };
 
 static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_steps) {
-  TilePlan pl{0, 0, 0, 0};
+  TilePlan pl{0, 0, 0, 0, 0};
   if (M < 1 || M > 16 || N < 1 || K < kStepK) return pl;
   if (getenv("MIQ_WO_STREAM")) return pl;  // force the streamed kernel (tuning, tests)
   // int8 with more than 2 rows: the streamed kernel measured faster on MI355X (the staged
@@ -332,6 +337,10 @@ static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_s
   const int64_t units = steps / us;
   if (us > kTileNS) return pl;
   const int64_t xbytes = M * (steps * kStepK + 8) * 2;
+  // rows per tile: enough tiles for every CU, at most 16 (MIQ_WO_ROWS overrides, tuning)
+  int rows = (int)std::min<int64_t>(16, (N + kCUs - 1) / kCUs);
+  if (const char* e = getenv("MIQ_WO_ROWS")) rows = std::max(1, std::min(16, atoi(e)));
+  const int64_t tiles = (N + rows - 1) / rows;
   for (int W : {4, 8, 16}) {
     if ((units + W - 1) / W * us > kTileNS) continue;
     const size_t lds = (size_t)std::max<int64_t>(xbytes, (int64_t)W * M * 16 * 4) + (size_t)steps * 16 * 4;
@@ -339,11 +348,12 @@ static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_s
     // every tile should be resident at once (a second wave of workgroups would stage the
     // activations again): workgroups per CU from LDS and from 16 wavefronts per CU
     const int64_t per_cu = std::min<int64_t>((int64_t)kTileLds / (int64_t)lds, 16 / W);
-    if ((N + 15) / 16 > per_cu * kCUs * 5 / 4) return pl;
+    if (tiles > per_cu * kCUs * 5 / 4) return pl;
     pl.W = W;
     pl.units = (int)units;
     pl.unit_steps = us;
     pl.lds_bytes = lds;
+    pl.rows = rows;
     return pl;
   }
   return pl;
@@ -374,10 +384,11 @@ int wo_tile_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, i
   p.steps = K / kStepK;
   p.units = pl.units;
   p.unit_steps = pl.unit_steps;
+  p.rows = pl.rows;
   p.wbytes = (int)((int64_t)N * ldw);
   const int esz = sd == MIQ_F32 ? 4 : 2;
   p.sbytes = kind == KIND_INT4 ? (int)(((int64_t)N * ngroups * esz + 3) & ~3LL) : 0;
-  const unsigned blocks = (unsigned)((N + 15) / 16);
+  const unsigned blocks = (unsigned)((N + pl.rows - 1) / pl.rows);
   if (kind == KIND_INT8) launch_tile_sd<KIND_INT8, false>(sd, pl.W, p, blocks, pl.lds_bytes, st);
   else if (zero) launch_tile_sd<KIND_INT4, true>(sd, pl.W, p, blocks, pl.lds_bytes, st);
   else launch_tile_sd<KIND_INT4, false>(sd, pl.W, p, blocks, pl.lds_bytes, st);

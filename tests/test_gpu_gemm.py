@@ -131,17 +131,22 @@ def test_w4a16_scale_dtypes(sdt):
 # Cases: multi-wavefront slices (K = 9728), an odd number of k-steps (K = 1152), groups of
 # 3 k-steps, long groups, f32 scales.
 TILE_CASES = [(1, 320, 9728, 128), (4, 320, 9728, 128), (3, 160, 1152, 128), (2, 96, 1152, 384),
-              (8, 64, 4096, 512), (16, 64, 1024, 128), (7, 48, 2560, 256)]
+              (8, 64, 4096, 512), (16, 64, 1024, 128), (7, 48, 2560, 256), (1, 2560, 9728, 128),
+              (5, 3008, 2048, 128)]
+# kernel choice: the default plan, the streamed kernel, and the tile kernel with a forced
+# number of weight rows per tile (16, and 7: a tile whose 128-byte loads are partly empty)
+KERNELS = {"auto": {}, "stream": {"MIQ_WO_STREAM": "1"}, "rows16": {"MIQ_WO_ROWS": "16"},
+           "rows7": {"MIQ_WO_ROWS": "7"}}
 
 
-@pytest.mark.parametrize("kernel", ["auto", "stream"])
+@pytest.mark.parametrize("kernel", list(KERNELS))
 @pytest.mark.parametrize("M,N,K,group", TILE_CASES)
 @pytest.mark.parametrize("sdt,symmetric", [(torch.bfloat16, True), (torch.float32, False), (torch.float16, False)])
 def test_w4a16_tile_and_stream(kernel, M, N, K, group, sdt, symmetric, monkeypatch):
     from kernels import quant_ops as ops
     case(f"w4a16 {kernel} M={M} N={N} K={K} g={group} {sdt} sym={symmetric}")
-    if kernel == "stream":
-        monkeypatch.setenv("MIQ_WO_STREAM", "1")
+    for k, v in KERNELS[kernel].items():
+        monkeypatch.setenv(k, v)
     w = make_w(N, K, 50)
     x = make_x(M, K, 51)
     q = O.int4_quantize_symmetric(w, group) if symmetric else O.int4_quantize(w, group)
@@ -154,13 +159,13 @@ def test_w4a16_tile_and_stream(kernel, M, N, K, group, sdt, symmetric, monkeypat
     within(y, want)
 
 
-@pytest.mark.parametrize("kernel", ["auto", "stream"])
-@pytest.mark.parametrize("M,N,K", [(1, 19456, 2560), (2, 4096, 2560), (3, 160, 1152), (4, 64, 9728)])
+@pytest.mark.parametrize("kernel", list(KERNELS))
+@pytest.mark.parametrize("M,N,K", [(1, 19456, 2560), (2, 4096, 2560), (3, 160, 1152), (4, 64, 9728), (1, 2512, 2560)])
 def test_w8a16_tile_and_stream(kernel, M, N, K, monkeypatch):
     from kernels import quant_ops as ops
     case(f"w8a16 {kernel} M={M} N={N} K={K}")
-    if kernel == "stream":
-        monkeypatch.setenv("MIQ_WO_STREAM", "1")
+    for k, v in KERNELS[kernel].items():
+        monkeypatch.setenv(k, v)
     w = make_w(N, K, 52)
     x = make_x(M, K, 53)
     q = O.int8_quantize(w, torch.float32)
