@@ -216,7 +216,7 @@ fp8_gemm32_kernel(const uint8_t* __restrict__ A, const float* __restrict__ sa,
                   const uint8_t* __restrict__ B, const float* __restrict__ sb,
                   uint16_t* __restrict__ Y, int64_t ldy, int M, int N, int K, int tiles_m,
                   int tiles_n, int xcd_panels) {
-  constexpr int kThreads = 256, WM = 2, WN = 2, NS = kStages32;
+  constexpr int WM = 2, WN = 2, NS = kStages32;  // 256 threads
   constexpr int kWaveM = BM / WM, kWaveN = BN / WN;    // 128 x 96
   constexpr int kTM = kWaveM / 32, kTN = kWaveN / 32;  // 4 x 3 tiles of 32 x 32
   constexpr int kRowBytes = BK32;                      // 64

@@ -438,13 +438,15 @@ paged_decode_split8_kernel(AttnParams p) {
   }
 
   // ---- the pieces of one chunk of CS x 32 tokens starting at c0
-  // K of 16 tokens comes in two loads of 8 tokens x 128 bytes (whole cache lines): load h
-  // reads token 8 h + (r & 7), 16-byte chunk ((r >> 3) ^ h) * 4 + g; k_swizzle turns the
-  // pair into token r, chunks g and 4 + g for lane (g, r)
+  // K of 16 tokens comes in two loads of 8 tokens x 128 bytes (whole cache lines), in
+  // address order within each 64-byte half: load h lane 32 c2 + 4 rr + cl reads token
+  // 8 h + rr, bytes 64 c2 + 16 cl; lanes_to_mfma turns the pair into token r, chunks g
+  // and 4 + g for lane (g, r)
   typedef int KSlots[CS][2];
   typedef int KLoadSlots[CS][2][2];
   typedef int VSlots[CS][4];
-  const int kchunk[2] = {((r >> 3) * 4 + g) * 16, (((r >> 3) ^ 1) * 4 + g) * 16};
+  const int lrr = (lane >> 2) & 7, kchunk = (lane >> 5) * 64 + (lane & 3) * 16;
+  const int bp_addr = (32 * (r >> 3) + 4 * (r & 7) + g) * 4;
   KLoadSlots kls;
   // chunk ci of the wavefront starts at token c0 (ci is a compile-time index where P16 uses it)
   auto lookup = [&](int c0, int ci, KSlots& ks, VSlots& vs) {  // K / P tokens c0 + 32 s + 16 c + r, V tokens c0 + 32 s + tq + i
@@ -456,7 +458,7 @@ paged_decode_split8_kernel(AttnParams p) {
           const int pg = wpage[ci * kPagesPerChunk + 2 * s + c];
           ks[s][c] = pg * 16 + r;
 #pragma unroll
-          for (int h = 0; h < 2; ++h) kls[s][c][h] = pg * 16 + 8 * h + (r & 7);
+          for (int h = 0; h < 2; ++h) kls[s][c][h] = pg * 16 + 8 * h + lrr;
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -472,7 +474,7 @@ paged_decode_split8_kernel(AttnParams p) {
       for (int c = 0; c < 2; ++c) {
         ks[s][c] = (int)slot_of(min(c0 + s * kStep + c * 16 + r, t_end - 1));
 #pragma unroll
-        for (int h = 0; h < 2; ++h) kls[s][c][h] = (int)slot_of(min(c0 + s * kStep + c * 16 + 8 * h + (r & 7), t_end - 1));
+        for (int h = 0; h < 2; ++h) kls[s][c][h] = (int)slot_of(min(c0 + s * kStep + c * 16 + 8 * h + lrr, t_end - 1));
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) vs[s][i] = (int)slot_of(min(c0 + s * kStep + tq + i, t_end - 1));
@@ -488,7 +490,7 @@ paged_decode_split8_kernel(AttnParams p) {
       for (int c = 0; c < 2; ++c) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
-          kr[bi][s][c][h] = *reinterpret_cast<const uint4*>(p.k + (int64_t)kls[s][c][h] * p.kvs_t + head_off + kchunk[h]);
+          kr[bi][s][c][h] = *reinterpret_cast<const uint4*>(p.k + (int64_t)kls[s][c][h] * p.kvs_t + head_off + kchunk);
         if (HAS_SCALE) ksr[bi][s][c] = load_sd_raw<SD>(p.ks, (int64_t)ks[s][c] * p.ss_t + (int64_t)kvh * p.ss_h);
       }
   };
@@ -504,15 +506,6 @@ paged_decode_split8_kernel(AttnParams p) {
       }
     }
   };
-  const bool lo_half = r < 8;
-  auto k_swizzle = [&](const uint4& i0, const uint4& i1, uint4& f0, uint4& f1) {
-    const uint4 a = lo_half ? i0 : i1, b2 = lo_half ? i1 : i0;
-    f0 = a;
-    f1.x = __builtin_amdgcn_update_dpp(0u, b2.x, 0x128, 0xf, 0xf, false);  // row_ror:8
-    f1.y = __builtin_amdgcn_update_dpp(0u, b2.y, 0x128, 0xf, 0xf, false);
-    f1.z = __builtin_amdgcn_update_dpp(0u, b2.z, 0x128, 0xf, 0xf, false);
-    f1.w = __builtin_amdgcn_update_dpp(0u, b2.w, 0x128, 0xf, 0xf, false);
-  };
   float sc[CS][2][4];
   // scores of the chunk (lane: heads 4 g + v of tokens c0 + 32 s + 16 c + r) and one
   // online-softmax update for all of them
@@ -524,7 +517,7 @@ paged_decode_split8_kernel(AttnParams p) {
         bf16x8 kf[4];
         uint32_t o[4];
         uint4 k0, k1;
-        k_swizzle(kr[bi][s][c][0], kr[bi][s][c][1], k0, k1);
+        lanes_to_mfma(bp_addr, kr[bi][s][c][0], kr[bi][s][c][1], k0, k1);
         bytes8_to_bf16<KVT>(k0.x, k0.y, o); kf[0] = bf16x8_from(o[0], o[1], o[2], o[3]);
         bytes8_to_bf16<KVT>(k0.z, k0.w, o); kf[1] = bf16x8_from(o[0], o[1], o[2], o[3]);
         bytes8_to_bf16<KVT>(k1.x, k1.y, o); kf[2] = bf16x8_from(o[0], o[1], o[2], o[3]);

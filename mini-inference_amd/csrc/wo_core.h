@@ -331,35 +331,5 @@ __device__ inline void stream_steps(const GroupQ<SD>& q, int M, const uint8_t* c
   }
 }
 
-// v gathered from lane addr / 4 (ds_bpermute: the LDS crossbar, no LDS memory)
-__device__ inline uint4 bpermute16(int addr, const uint4& v) {
-  uint4 o;
-  o.x = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)v.x);
-  o.y = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)v.y);
-  o.z = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)v.z);
-  o.w = (uint32_t)__builtin_amdgcn_ds_bpermute(addr, (int)v.w);
-  return o;
-}
-
-// Two loads in address order (lane 32 c2 + 4 rr + cl: row 8h + rr of load h, bytes
-// 64 c2 + 16 cl) to the MFMA layout: f0 = the first 64-byte half (c2 = 0), f1 = the
-// second, lane (g, r) holding row r, chunk g. The 32-lane swap makes register j hold half
-// c2 = j with lane bit 5 = h; one gather per dword then rotates the lane bits.
-__device__ inline void lanes_to_mfma(int addr, const uint4& l0, const uint4& l1, uint4& f0, uint4& f1) {
-  uint4 a, b;
-  const uint32_t* p0 = &l0.x;
-  const uint32_t* p1 = &l1.x;
-  uint32_t* pa = &a.x;
-  uint32_t* pb = &b.x;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const auto s = __builtin_amdgcn_permlane32_swap(p0[i], p1[i], false, false);
-    pa[i] = s[0];
-    pb[i] = s[1];
-  }
-  f0 = bpermute16(addr, a);
-  f1 = bpermute16(addr, b);
-}
-
 }  // namespace wo
 }  // namespace miq
