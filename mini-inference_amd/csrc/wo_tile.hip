@@ -67,7 +67,7 @@ struct TileParams {
   int wbytes, sbytes;
 };
 
-template <int KIND, bool HZ, int SD, int W>
+template <int KIND, bool HZ, int SD, int W, bool G1>
 __global__ void __launch_bounds__(W * 64)
 wo_tile_kernel(TileParams p) {
   constexpr int kThreads = W * 64, NS = kTileNS, XP = tile_xp<KIND>();
@@ -176,7 +176,9 @@ wo_tile_kernel(TileParams p) {
 
   MIQ_TRACE(1);
   // ---- stage the activations: LDS x [M][K + 8] bf16 (int4: pieces permuted for the
-  // unpack order), then xsum [steps][16] fp32, the sum of each row over each k-step
+  // unpack order), then xsum [steps][16] fp32, the sum of each row over each k-step times
+  // the code bias kXBias (the MFMA sees codes as 128 + u; symmetric int4 weights are u - 8)
+  constexpr float kXBias = KIND == KIND_INT4 && !HZ ? -136.f : -128.f;
   const int xstride = p.steps * kStepK + 8;
   float* xsum = reinterpret_cast<float*>(lds + M * xstride);
   for (int base = 0; base < npieces; base += XP * kThreads) {
@@ -194,13 +196,14 @@ wo_tile_kernel(TileParams p) {
       sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x112, 0xf, 0xf, true));
       sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x114, 0xf, 0xf, true));
       sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x118, 0xf, 0xf, true));
-      if (i < npieces && (c & 15) == 15) xsum[(c >> 4) * 16 + m] = sm;
+      if (i < npieces && (c & 15) == 15) xsum[(c >> 4) * 16 + m] = sm * kXBias;
     }
   }
   __syncthreads();
   MIQ_TRACE(2);
 
-  // ---- multiply the slice
+  // ---- multiply the slice. Per quantization group, T = sum_k x (128 + u) + kXBias * sum_k x
+  // (two MFMA chains and the staged sums), and acc += s * T (+ z * sum_k x with zero points)
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
   f32x4 acc = z4, accg = z4, acc2 = z4, xsg = z4;
   int c_grp = 0, c_left = p.group_steps;
@@ -216,7 +219,7 @@ wo_tile_kernel(TileParams p) {
         const uint4 v = *reinterpret_cast<const uint4*>(xrow + a_off<KIND>(kl, g, j));
         av[j] = as_bf16x8(v.x, v.y, v.z, v.w);
       }
-      xsg += *reinterpret_cast<const f32x4*>(xsum + kl * 16 + g * 4);
+      const f32x4 xb = *reinterpret_cast<const f32x4*>(xsum + kl * 16 + g * 4);
       uint4 wl[2];
       if (KIND == KIND_INT8) {
         lanes_to_mfma(bp_addr, wq[d][0], wq[d][1], wl[0], wl[1]);
@@ -227,20 +230,32 @@ wo_tile_kernel(TileParams p) {
       }
       bf16x8 bv[4];
       unpack_b<KIND>(wl, bv);
+      if (KIND == KIND_INT4 && G1) {
+        // one-step groups: the first chain starts from the step's bias, the second from
+        // zero, and the group ends here (scale and zero of group d: compile-time indices)
+        accg = mfma(av[0], bv[0], xb);
+        acc2 = mfma(av[1], bv[1], z4);
+        accg = mfma(av[2], bv[2], accg);
+        acc2 = mfma(av[3], bv[3], acc2);
+        const float sc = group_value(sw, d);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        f32x4& chain = (j & 1) ? acc2 : (KIND == KIND_INT4 ? accg : acc);
-        chain = mfma(av[j], bv[j], chain);
-      }
-      if (KIND == KIND_INT4 && --c_left == 0) {  // end of a quantization group
-        // group d of the slice for one-step groups (a compile-time index), else c_grp
-        // picked by a select chain (a run-time index into the word array would spill it)
-        float sc, zv = 0.f;
-        if (p.group_steps == 1) {
-          sc = group_value(sw, d);
-          if (HZ) zv = group_value(zw, d);
-        } else {
-          sc = group_value(sw, 0);
+        for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(sc, accg[v] + acc2[v], acc[v]);
+        if (HZ) {
+          const float zq = group_value(zw, d) * (1.f / kXBias);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(zq, xb[v], acc[v]);
+        }
+      } else {
+        xsg += xb;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          f32x4& chain = (j & 1) ? acc2 : (KIND == KIND_INT4 ? accg : acc);
+          chain = mfma(av[j], bv[j], chain);
+        }
+        if (KIND == KIND_INT4 && --c_left == 0) {  // end of a quantization group
+          // group c_grp picked by a select chain (a run-time index into the word array
+          // would spill it)
+          float sc = group_value(sw, 0), zv = 0.f;
           if (HZ) zv = group_value(zw, 0);
 #pragma unroll
           for (int e = 1; e < NS; ++e) {
@@ -248,21 +263,25 @@ wo_tile_kernel(TileParams p) {
             sc = c_grp == e ? group_value(sw, e) : sc;
             if (HZ) zv = c_grp == e ? group_value(zw, e) : zv;
           }
-        }
-        const float cz = HZ ? zv - 128.f * sc : -136.f * sc;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[v] += sc * (accg[v] + acc2[v]) + cz * xsg[v];
-        accg = z4;
-        acc2 = z4;
-        xsg = z4;
-        ++c_grp;
-        c_left = p.group_steps;
+          for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(sc, accg[v] + acc2[v] + xsg[v], acc[v]);
+          if (HZ) {
+            const float zq = zv * (1.f / kXBias);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(zq, xsg[v], acc[v]);
+          }
+          accg = z4;
+          acc2 = z4;
+          xsg = z4;
+          ++c_grp;
+          c_left = p.group_steps;
+        }
       }
     }
   }
   if (KIND == KIND_INT8) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) acc[v] += acc2[v] - 128.f * xsg[v];
+    for (int v = 0; v < 4; ++v) acc[v] += acc2[v] + xsg[v];
   }
 
   MIQ_TRACE(3);
@@ -288,15 +307,22 @@ wo_tile_kernel(TileParams p) {
   MIQ_TRACE(4);
 }
 
-template <int KIND, bool HZ, int SD, int W>
-void launch_tile(const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
+template <int KIND, bool HZ, int SD, int W, bool G1>
+void launch_tile_g(const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wo_tile_kernel<KIND, HZ, SD, W>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wo_tile_kernel<KIND, HZ, SD, W, G1>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, kTileLds);
     attr = true;
   }
-  hipLaunchKernelGGL((wo_tile_kernel<KIND, HZ, SD, W>), dim3(blocks), dim3(W * 64), lds, st, p);
+  hipLaunchKernelGGL((wo_tile_kernel<KIND, HZ, SD, W, G1>), dim3(blocks), dim3(W * 64), lds, st, p);
+}
+
+// int4 with one-step (128-code) groups has its own instantiation
+template <int KIND, bool HZ, int SD, int W>
+void launch_tile(const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
+  if (KIND == KIND_INT4 && p.group_steps == 1) launch_tile_g<KIND, HZ, SD, W, true>(p, blocks, lds, st);
+  else launch_tile_g<KIND, HZ, SD, W, false>(p, blocks, lds, st);
 }
 
 template <int KIND, bool HZ, int SD>
