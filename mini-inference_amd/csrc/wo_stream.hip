@@ -94,7 +94,7 @@ struct StreamParams {
   int* counters;        // [kMaxCounters]
 };
 
-template <int KIND, bool HZ, int SD, int MT, int NR>
+template <int KIND, bool HZ, int SD, int MT, int NR, bool G1>
 __global__ void __launch_bounds__(waves_for<MT>() * 64)
 wo_stream_kernel(StreamParams p_in) {
   // M split (grid.z > 1, one activation tile each): this workgroup's 16 rows of x and y,
@@ -237,6 +237,10 @@ wo_stream_kernel(StreamParams p_in) {
 
   // two MFMA accumulation chains per tile (even / odd j), so consecutive MFMAs do not
   // wait for each other's results
+  // Per quantization group, T = sum_k x (128 + u) + kXBias * sum_k x (two MFMA chains and
+  // the staged sums, which hold kXBias times the sum of x over each k-step), and
+  // acc += s * T (+ z * sum_k x with zero points)
+  constexpr float kXBias = KIND == KIND_INT4 && !HZ ? -136.f : -128.f;
   f32x4 acc[NR][MT], accg[NR][MT], acc2[NR][MT], xsg[MT];
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -279,7 +283,7 @@ wo_stream_kernel(StreamParams p_in) {
         sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x112, 0xf, 0xf, true));
         sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x114, 0xf, 0xf, true));
         sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x118, 0xf, 0xf, true));
-        if (i < npieces && (c & 15) == 15) xsum[(c >> 4) * XR + m] = sm;
+        if (i < npieces && (c & 15) == 15) xsum[(c >> 4) * XR + m] = sm * kXBias;
       }
     }
     for (int base = 0; base < (KIND == KIND_INT8 && MT >= 2 ? 0 : npieces); base += XP * kThreads) {
@@ -298,7 +302,7 @@ wo_stream_kernel(StreamParams p_in) {
         sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x112, 0xf, 0xf, true));
         sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x114, 0xf, 0xf, true));
         sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x118, 0xf, 0xf, true));
-        if (i < npieces && (c & 15) == 15) xsum[(c >> 4) * XR + m] = sm;
+        if (i < npieces && (c & 15) == 15) xsum[(c >> 4) * XR + m] = sm * kXBias;
       }
     }
     __syncthreads();
@@ -311,6 +315,7 @@ wo_stream_kernel(StreamParams p_in) {
         const int kst = k + d, kl = kst - c0;
         if (kst < c0 + nst) {
           bf16x8 av[MT][4];
+          f32x4 xb[MT];
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
             const uint16_t* row = lds + min(mt * 16 + r, M - 1) * xstride;
@@ -319,7 +324,8 @@ wo_stream_kernel(StreamParams p_in) {
               const uint4 v = *reinterpret_cast<const uint4*>(row + a_off<KIND>(kl, g, j));
               av[mt][j] = as_bf16x8(v.x, v.y, v.z, v.w);
             }
-            xsg[mt] += *reinterpret_cast<const f32x4*>(xsum + kl * XR + mt * 16 + g * 4);
+            xb[mt] = *reinterpret_cast<const f32x4*>(xsum + kl * XR + mt * 16 + g * 4);
+            if (!G1) xsg[mt] += xb[mt];
           }
 #pragma unroll
           for (int t = 0; t < NR; ++t) {
@@ -333,6 +339,27 @@ wo_stream_kernel(StreamParams p_in) {
               wl[0] = wnext[t];
             }
             unpack_b<KIND>(wl, bv);
+            if (G1) {
+              // one-step groups: the first chain starts from the step's bias, the second
+              // from zero, and the group ends here
+              const int gi = soff[t] + c_grp;
+              const float sc = word_to_f32<SD>(sq[d][t], gi);
+              const float zs = HZ ? word_to_f32<SD>(zq[d][t], gi) * (1.f / kXBias) : 0.f;
+#pragma unroll
+              for (int mt = 0; mt < MT; ++mt) {
+                f32x4 c0v = mfma(av[mt][0], bv[0], xb[mt]);
+                f32x4 c1v = mfma(av[mt][1], bv[1], z4);
+                c0v = mfma(av[mt][2], bv[2], c0v);
+                c1v = mfma(av[mt][3], bv[3], c1v);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[t][mt][v] = __builtin_fmaf(sc, c0v[v] + c1v[v], acc[t][mt][v]);
+                if (HZ) {
+#pragma unroll
+                  for (int v = 0; v < 4; ++v) acc[t][mt][v] = __builtin_fmaf(zs, xb[mt][v], acc[t][mt][v]);
+                }
+              }
+              continue;
+            }
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -341,16 +368,22 @@ wo_stream_kernel(StreamParams p_in) {
                 chain = mfma(av[mt][j], bv[j], chain);
               }
           }
-          if (KIND == KIND_INT4 && --c_left == 0) {  // end of a quantization group
+          if (G1) {
+            ++c_grp;
+          } else if (KIND == KIND_INT4 && --c_left == 0) {  // end of a quantization group
 #pragma unroll
             for (int t = 0; t < NR; ++t) {
               const int gi = soff[t] + c_grp;
               const float sc = word_to_f32<SD>(sq[d][t], gi);
-              const float cz = HZ ? word_to_f32<SD>(zq[d][t], gi) - 128.f * sc : -136.f * sc;
+              const float zs = HZ ? word_to_f32<SD>(zq[d][t], gi) * (1.f / kXBias) : 0.f;
 #pragma unroll
               for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
-                for (int v = 0; v < 4; ++v) acc[t][mt][v] += sc * (accg[t][mt][v] + acc2[t][mt][v]) + cz * xsg[mt][v];
+                for (int v = 0; v < 4; ++v) acc[t][mt][v] = __builtin_fmaf(sc, accg[t][mt][v] + acc2[t][mt][v] + xsg[mt][v], acc[t][mt][v]);
+                if (HZ) {
+#pragma unroll
+                  for (int v = 0; v < 4; ++v) acc[t][mt][v] = __builtin_fmaf(zs, xsg[mt][v], acc[t][mt][v]);
+                }
                 accg[t][mt] = z4;
                 acc2[t][mt] = z4;
               }
@@ -371,7 +404,7 @@ wo_stream_kernel(StreamParams p_in) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[t][mt][v] += acc2[t][mt][v] - 128.f * xsg[mt][v];
+        for (int v = 0; v < 4; ++v) acc[t][mt][v] += acc2[t][mt][v] + xsg[mt][v];
   }
 
   MIQ_TRACE(3);
@@ -522,8 +555,6 @@ StreamPlan plan_stream(int kind, int64_t M, int64_t N, int64_t K, int group_step
   const int64_t rows = (pl.MT == 1 ? waves_for<1>() : waves_for<2>()) * pl.NR * 16;
   pl.blocks = (int)((N + rows - 1) / rows);
   if (S == 0) {
-    // about 2 workgroups per CU for one tile of activation rows, about 1.5 for more
-    // rows (measured on MI355X over the Qwen3 projection shapes)
     // one activation tile: splits of about 8 k-steps; more tiles: about 1.5 workgroups
     // per CU (measured on MI355X over the Qwen3 projection shapes)
     if (pl.MT == 1) {
@@ -548,15 +579,22 @@ StreamPlan plan_stream(int kind, int64_t M, int64_t N, int64_t K, int group_step
   return pl;
 }
 
-template <int KIND, bool HZ, int SD, int MT, int NR>
-void launch_stream(const StreamParams& p, dim3 grid, size_t lds, hipStream_t st) {
+template <int KIND, bool HZ, int SD, int MT, int NR, bool G1>
+void launch_stream_g(const StreamParams& p, dim3 grid, size_t lds, hipStream_t st) {
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wo_stream_kernel<KIND, HZ, SD, MT, NR>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wo_stream_kernel<KIND, HZ, SD, MT, NR, G1>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBudget);
     attr = true;
   }
-  hipLaunchKernelGGL((wo_stream_kernel<KIND, HZ, SD, MT, NR>), grid, dim3(waves_for<MT>() * 64), lds, st, p);
+  hipLaunchKernelGGL((wo_stream_kernel<KIND, HZ, SD, MT, NR, G1>), grid, dim3(waves_for<MT>() * 64), lds, st, p);
+}
+
+// int4 with one-step (128-code) groups has its own instantiation
+template <int KIND, bool HZ, int SD, int MT, int NR>
+void launch_stream(const StreamParams& p, dim3 grid, size_t lds, hipStream_t st) {
+  if (KIND == KIND_INT4 && p.group_steps == 1) launch_stream_g<KIND, HZ, SD, MT, NR, true>(p, grid, lds, st);
+  else launch_stream_g<KIND, HZ, SD, MT, NR, false>(p, grid, lds, st);
 }
 
 template <int KIND, bool HZ, int SD>
