@@ -264,7 +264,7 @@ constexpr int kMoeChunk = 16;  // k-steps of activations staged at once
 #endif
 constexpr int kItemsPerRun = MIQ_MOE_RUN;  // consecutive items per workgroup (one staging)
 
-template <int MODE, bool HZ, int SD>
+template <int MODE, bool HZ, int SD, bool G1>
 __global__ void __launch_bounds__(256)
 moe_stream_kernel(MoeParams p, int blocks_per_tile) {
   extern __shared__ __align__(16) uint16_t lds[];
@@ -362,11 +362,16 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
     __syncthreads();  // s_src ready (and the previous item is done with LDS)
 
     uint4 wnext[NR];
+    // Per quantization group, T = sum_k x (128 + u) + kXBias * sum_k x (MFMA chains and the
+    // staged sums, which hold kXBias times the sum of x over each k-step), and
+    // acc += s * T (+ z * sum_k x with zero points)
+    constexpr float kXBias = HZ ? -128.f : -136.f;
     f32x4 acc[NR], accg[NR], xsg;
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < NR; ++t) { acc[t] = z4; accg[t] = z4; }
     xsg = z4;
+    int c_grp = 0, c_left = p.group_steps;  // group of the next k-step and its steps left
 
     for (int c0 = 0; c0 < steps; c0 += kMoeChunk) {
       const int nst = min(kMoeChunk, steps - c0);
@@ -394,7 +399,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
           sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x112, 0xf, 0xf, true));
           sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x114, 0xf, 0xf, true));
           sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x118, 0xf, 0xf, true));
-          if (i < npieces && (c & 15) == 15) xsum[(c >> 4) * kTile + m] = sm;
+          if (i < npieces && (c & 15) == 15) xsum[(c >> 4) * kTile + m] = sm * kXBias;
         }
       }
       __syncthreads();
@@ -410,7 +415,8 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
               const uint4 v = *reinterpret_cast<const uint4*>(arow + a_off<KIND_INT4>(kl, g, j));
               av[j] = as_bf16x8(v.x, v.y, v.z, v.w);
             }
-            xsg += *reinterpret_cast<const f32x4*>(xsum + kl * kTile + g * 4);
+            const f32x4 xb = *reinterpret_cast<const f32x4*>(xsum + kl * kTile + g * 4);
+            if (!G1) xsg += xb;
 #pragma unroll
             for (int t = 0; t < NR; ++t) {
               bf16x8 bv[4];
@@ -418,20 +424,45 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
               if ((d & 1) == 0) lanes_to_mfma(bp_addr, wq[d][t][0], wq[d + 1][t][0], wl, wnext[t]);
               else wl = wnext[t];
               unpack_b<KIND_INT4>(&wl, bv);
+              if (G1) {
+                // one-step groups: chains from the step's bias and from zero; the group ends here
+                const int gi = soff[t] + c_grp;
+                const float sc = word_to_f32<SD>(sq[d][t], gi);
+                f32x4 c0v = mfma(av[0], bv[0], xb);
+                f32x4 c1v = mfma(av[1], bv[1], z4);
+                c0v = mfma(av[2], bv[2], c0v);
+                c1v = mfma(av[3], bv[3], c1v);
 #pragma unroll
-              for (int j = 0; j < 4; ++j) accg[t] = mfma(av[j], bv[j], accg[t]);
+                for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(sc, c0v[v] + c1v[v], acc[t][v]);
+                if (HZ) {
+                  const float zs = word_to_f32<SD>(zq[d][t], gi) * (1.f / kXBias);
+#pragma unroll
+                  for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(zs, xb[v], acc[t][v]);
+                }
+              } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) accg[t] = mfma(av[j], bv[j], accg[t]);
+              }
             }
-            if ((kst + 1) % p.group_steps == 0) {
+            if (G1) {
+              ++c_grp;
+            } else if (--c_left == 0) {  // end of a quantization group
 #pragma unroll
               for (int t = 0; t < NR; ++t) {
-                const int gi = soff[t] + kst / p.group_steps;
+                const int gi = soff[t] + c_grp;
                 const float sc = word_to_f32<SD>(sq[d][t], gi);
-                const float cz = HZ ? word_to_f32<SD>(zq[d][t], gi) - 128.f * sc : -136.f * sc;
 #pragma unroll
-                for (int v = 0; v < 4; ++v) acc[t][v] += sc * accg[t][v] + cz * xsg[v];
+                for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(sc, accg[t][v] + xsg[v], acc[t][v]);
+                if (HZ) {
+                  const float zs = word_to_f32<SD>(zq[d][t], gi) * (1.f / kXBias);
+#pragma unroll
+                  for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(zs, xsg[v], acc[t][v]);
+                }
                 accg[t] = z4;
               }
               xsg = z4;
+              ++c_grp;
+              c_left = p.group_steps;
             }
           }
           request(d, kst + D);
@@ -466,8 +497,8 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
   }
 }
 
-template <bool HZ, int SD>
-void launch_stream_experts(const MoeParams& p, int max_tiles, hipStream_t st) {
+template <bool HZ, int SD, bool G1>
+void launch_stream_experts_g(const MoeParams& p, int max_tiles, hipStream_t st) {
   const int steps_gu = p.H / kStepK, steps_dn = p.I / kStepK;
   const size_t lds_gu = (size_t)kTile * (kMoeChunk * kStepK + 8) * 2 + (size_t)kMoeChunk * kTile * 4;
   const int bgu = p.I / 64, bdn = p.H / 128;
@@ -475,17 +506,24 @@ void launch_stream_experts(const MoeParams& p, int max_tiles, hipStream_t st) {
   (void)steps_dn;
   static bool attr = false;
   if (!attr) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_stream_kernel<MOE_GU, HZ, SD>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_stream_kernel<MOE_GU, HZ, SD, G1>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_gu);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_stream_kernel<MOE_DN, HZ, SD>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_stream_kernel<MOE_DN, HZ, SD, G1>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_gu);
     attr = true;
   }
   // about two workgroups per CU, never more than the runs of items that could exist
   const int grid_gu = std::max(1, std::min(512, max_tiles * bgu / kItemsPerRun));
   const int grid_dn = std::max(1, std::min(512, max_tiles * bdn / kItemsPerRun));
-  hipLaunchKernelGGL((moe_stream_kernel<MOE_GU, HZ, SD>), dim3(grid_gu), dim3(256), lds_gu, st, p, bgu);
-  hipLaunchKernelGGL((moe_stream_kernel<MOE_DN, HZ, SD>), dim3(grid_dn), dim3(256), lds_gu, st, p, bdn);
+  hipLaunchKernelGGL((moe_stream_kernel<MOE_GU, HZ, SD, G1>), dim3(grid_gu), dim3(256), lds_gu, st, p, bgu);
+  hipLaunchKernelGGL((moe_stream_kernel<MOE_DN, HZ, SD, G1>), dim3(grid_dn), dim3(256), lds_gu, st, p, bdn);
+}
+
+// one-step (128-code) groups have their own instantiation
+template <bool HZ, int SD>
+void launch_stream_experts(const MoeParams& p, int max_tiles, hipStream_t st) {
+  if (p.group_steps == 1) launch_stream_experts_g<HZ, SD, true>(p, max_tiles, st);
+  else launch_stream_experts_g<HZ, SD, false>(p, max_tiles, st);
 }
 
 // out[t][n] = sum over slots j (in order) of ypair[t * k + j][n]
