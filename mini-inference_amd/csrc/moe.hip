@@ -5,8 +5,9 @@
 // moe_align contract (as in the reference): the T*k (token, slot) pairs are grouped by
 // expert, each group padded to a multiple of block_m with the sentinel T*k, expert_ids
 // names the expert of each block_m-row tile (tiles past the end get E - 1), num_padded
-// is the used length. Here the pairs inside a group are in ascending pair order: one
-// wavefront per expert walks the pairs with ballots, so the layout is deterministic.
+// is the used length. Here the pairs inside a group are in ascending pair order, so the
+// layout is deterministic: per-chunk ranks from ballots (moe_align_chunks_kernel) or, for
+// sizes whose chunk tables do not fit in LDS, one wavefront per expert walking the pairs.
 //
 // The grouped GEMMs reuse the weight-only core (wo_core.h): a workgroup takes one
 // 16-row tile of one expert, gathers its activation rows into LDS, and its four
@@ -93,6 +94,96 @@ moe_align_kernel(const void* __restrict__ ids, int dtype, int num_pairs, int E, 
       if (hit) sorted_ids[base + __popcll(mask & below)] = i;
       base += __popcll(mask);
     }
+  }
+}
+
+// The same contract for sizes whose per-chunk tables fit in LDS, with fewer dependent
+// steps: every wavefront takes chunks of 64 pairs; a pair's rank among the pairs of its
+// expert in the chunk comes from one ballot per bit of the expert id (lanes agreeing on
+// every bit are the same expert); per-expert prefix sums over the chunks then give every
+// pair its slot directly. Pairs of an expert stay in ascending pair order.
+__global__ void __launch_bounds__(1024)
+moe_align_chunks_kernel(const void* __restrict__ ids, int dtype, int num_pairs, int E, int bm, int max_padded,
+                        int max_blocks, int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
+                        int32_t* __restrict__ num_padded) {
+  extern __shared__ int sm[];
+  const int nch = (num_pairs + 63) / 64;
+  int* counts = sm;                  // [E]
+  int* offsets = sm + E;             // [E + 1]
+  int* cc = sm + 2 * E + 1;          // [nch][E] pairs of expert e in chunk c, then their start in the group
+  int* rk = cc + nch * E;            // [nch * 64] rank in the chunk among the expert's pairs (-1: no expert)
+  int* le = rk + nch * 64;           // [nch * 64] expert of the pair
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), nw = blockDim.x >> 6;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int nbits = 32 - __builtin_clz((unsigned)E);  // ids 0 .. E (E: out of range)
+  for (int i = tid; i < nch * E; i += blockDim.x) cc[i] = 0;
+  __syncthreads();
+  for (int c = wv; c < nch; c += nw) {
+    const int i = c * 64 + lane;
+    int e = i < num_pairs ? load_id(ids, dtype, i) : E;
+    if (e < 0 || e >= E) e = E;
+    uint64_t peers = ~0ull;
+    for (int b = 0; b < nbits; ++b) {
+      const bool bit = (e >> b) & 1;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    const int rank = __popcll(peers & below);
+    rk[i] = e < E ? rank : -1;
+    le[i] = e;
+    if (e < E && rank == 0) cc[c * E + e] = __popcll(peers);
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += blockDim.x) {  // exclusive prefix over the chunks
+    int run = 0;
+    for (int c = 0; c < nch; ++c) {
+      const int t = cc[c * E + e];
+      cc[c * E + e] = run;
+      run += t;
+    }
+    counts[e] = run;
+  }
+  __syncthreads();
+  if (wv == 0) {  // exclusive scan of the padded counts, 64 experts per round
+    int carry = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      const int c = e < E ? (counts[e] + bm - 1) / bm * bm : 0;
+      int incl = c;
+      for (int o = 1; o < 64; o <<= 1) {
+        const int up = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += up;
+      }
+      if (e < E) offsets[e] = carry + incl - c;
+      carry += __shfl(incl, 63, 64);
+    }
+    if (lane == 0) {
+      offsets[E] = carry;
+      *num_padded = carry;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < max_padded; i += blockDim.x) sorted_ids[i] = num_pairs;
+  for (int t = tid; t < max_blocks; t += blockDim.x) {
+    const int row = t * bm;
+    int owner = E - 1;
+    if (row < offsets[E]) {
+      int lo = 0, hi = E - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi) / 2;
+        if (offsets[mid + 1] <= row) lo = mid + 1;
+        else hi = mid;
+      }
+      owner = lo;
+    }
+    expert_ids[t] = owner;
+  }
+  __syncthreads();  // the sentinel fill lands before the pairs are placed
+  for (int i = tid; i < nch * 64; i += blockDim.x) {
+    const int r = rk[i];
+    if (r < 0) continue;
+    const int e = le[i];
+    sorted_ids[offsets[e] + cc[(i >> 6) * E + e] + r] = i;
   }
 }
 
@@ -578,6 +669,14 @@ extern "C" int miq_moe_align(const void* topk_ids, int idx_dtype, int64_t num_pa
               (long long)block_m);
   const int64_t max_padded = num_pairs + E * (block_m - 1);
   const int64_t max_blocks = (max_padded + block_m - 1) / block_m;
+  const int64_t nch = (num_pairs + 63) / 64;
+  const int64_t chunk_ints = 2 * E + 1 + nch * E + nch * 128;
+  if (chunk_ints * 4 <= 64 * 1024 && !getenv("MIQ_MOE_ALIGN_SCAN")) {
+    hipLaunchKernelGGL(moe_align_chunks_kernel, dim3(1), dim3(1024), (size_t)chunk_ints * sizeof(int),
+                       (hipStream_t)stream, topk_ids, idx_dtype, (int)num_pairs, (int)E, (int)block_m,
+                       (int)max_padded, (int)max_blocks, sorted_ids, expert_ids, num_padded);
+    return check_launch("moe_align");
+  }
   const int in_lds = (2 * E + 1 + num_pairs) * 4 <= 64 * 1024;
   hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(1024), (size_t)(2 * E + 1 + (in_lds ? num_pairs : 0)) * sizeof(int),
                      (hipStream_t)stream, topk_ids, idx_dtype, (int)num_pairs, (int)E, (int)block_m,

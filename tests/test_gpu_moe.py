@@ -20,12 +20,17 @@ def rel_error(a, b):
 @pytest.mark.parametrize("T,k,E,bm", [(1, 8, 64, 16), (13, 3, 8, 4), (16, 8, 64, 16), (300, 8, 64, 32),
                                        (4096, 8, 64, 64), (64, 8, 64, 16)])
 @pytest.mark.parametrize("dtype", [torch.int64, torch.int32])
-def test_moe_align_matches_oracle_exactly(T, k, E, bm, dtype):
+@pytest.mark.parametrize("path", ["auto", "scan"])
+def test_moe_align_matches_oracle_exactly(T, k, E, bm, dtype, path, monkeypatch):
     """The HIP kernel places pairs in ascending order inside each expert, so its output
     equals the oracle's stable restatement element for element (a stronger check than the
-    grouping equality of reference tests/test_fused_moe.py:56-88)."""
+    grouping equality of reference tests/test_fused_moe.py:56-88). "auto" takes the
+    per-chunk kernel where its tables fit in LDS (all but T=4096 here), "scan" forces the
+    one-wavefront-per-expert kernel."""
     from kernels.fused_moe import moe_align
-    case(f"moe_align T={T} k={k} E={E} bm={bm} {dtype}")
+    if path == "scan":
+        monkeypatch.setenv("MIQ_MOE_ALIGN_SCAN", "1")
+    case(f"moe_align T={T} k={k} E={E} bm={bm} {dtype} {path}")
     g = torch.Generator().manual_seed(T)
     ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(dtype)
     s, e, n = moe_align(ids.to(DEV), E, bm)
