@@ -202,7 +202,7 @@ struct MoeParams {
   const int32_t* expert_ids;
   const int32_t* num_padded;
   uint16_t* hbuf;  // [max_padded, I] bf16: silu(gate) * up per sorted row
-  float* ypair;    // [num_pairs, H] fp32: routed down-projection per pair
+  uint16_t* ypair;  // [num_pairs, H] bf16: routed down-projection per pair (bf16-rounded values)
   uint16_t* out;   // [T, H]
 };
 
@@ -329,7 +329,7 @@ moe_down_kernel(MoeParams p, int chunk_steps) {
     const int pair = p.sorted_ids[tile * kTile + m];
     if (pair < p.num_pairs) {
       const float w = bf16_to_f32(p.topk_w[pair]);
-      p.ypair[(int64_t)pair * p.H + n] = bf16r(bf16r(acc[v]) * w);
+      p.ypair[(int64_t)pair * p.H + n] = f32_to_bf16(bf16r(bf16r(acc[v]) * w));
     }
   }
 }
@@ -580,8 +580,8 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
         if (pair < p.num_pairs) {
           const float w = bf16_to_f32(p.topk_w[pair]);
           const int n0 = blk * 128 + wv * 32 + r;
-          p.ypair[(int64_t)pair * p.H + n0] = bf16r(bf16r(acc[0][v]) * w);
-          p.ypair[(int64_t)pair * p.H + n0 + 16] = bf16r(bf16r(acc[1][v]) * w);
+          p.ypair[(int64_t)pair * p.H + n0] = f32_to_bf16(bf16r(bf16r(acc[0][v]) * w));
+          p.ypair[(int64_t)pair * p.H + n0 + 16] = f32_to_bf16(bf16r(bf16r(acc[1][v]) * w));
         }
       }
     }
@@ -617,14 +617,24 @@ void launch_stream_experts(const MoeParams& p, int max_tiles, hipStream_t st) {
   else launch_stream_experts_g<HZ, SD, false>(p, max_tiles, st);
 }
 
-// out[t][n] = sum over slots j (in order) of ypair[t * k + j][n]
-__global__ void moe_combine_kernel(const float* __restrict__ ypair, int topk, int H, uint16_t* __restrict__ out) {
+// out[t][n] = sum over slots j (in order) of ypair[t * k + j][n] in fp32; four consecutive
+// n per thread (H is a multiple of 64)
+__global__ void moe_combine_kernel(const uint16_t* __restrict__ ypair, int topk, int H, uint16_t* __restrict__ out) {
   const int t = blockIdx.y;
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (n >= H) return;
-  float s = 0.f;
-  for (int j = 0; j < topk; ++j) s += ypair[((int64_t)t * topk + j) * H + n];
-  out[(int64_t)t * H + n] = f32_to_bf16(s);
+  float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+  const uint16_t* row = ypair + (int64_t)t * topk * H + n;
+  for (int j = 0; j < topk; ++j) {
+    const uint2 v = *reinterpret_cast<const uint2*>(row + (int64_t)j * H);
+    s.x += __builtin_bit_cast(float, v.x << 16);
+    s.y += __builtin_bit_cast(float, v.x & 0xffff0000u);
+    s.z += __builtin_bit_cast(float, v.y << 16);
+    s.w += __builtin_bit_cast(float, v.y & 0xffff0000u);
+  }
+  const uint32_t lo = f32_to_bf16(s.x) | ((uint32_t)f32_to_bf16(s.y) << 16);
+  const uint32_t hi = f32_to_bf16(s.z) | ((uint32_t)f32_to_bf16(s.w) << 16);
+  *reinterpret_cast<uint2*>(out + (int64_t)t * H + n) = make_uint2(lo, hi);
 }
 
 template <bool HZ, int SD>
@@ -686,7 +696,7 @@ extern "C" int miq_moe_align(const void* topk_ids, int idx_dtype, int64_t num_pa
 
 extern "C" size_t miq_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I) {
   const size_t hb = max_padded_rows(T * topk, E) * (size_t)I * 2;
-  return ((hb + 255) / 256) * 256 + (size_t)T * topk * H * 4;
+  return ((hb + 255) / 256) * 256 + (size_t)T * topk * H * 2;
 }
 
 extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
@@ -709,6 +719,8 @@ extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I
               "w4a16_moe: expert weights above 2 GiB");
   const size_t need = miq_moe_workspace_bytes(T, topk, E, H, I);
   MIQ_REQUIRE(workspace != nullptr && workspace_bytes >= need, "w4a16_moe: workspace of %zu bytes needed", need);
+  MIQ_REQUIRE(((reinterpret_cast<uintptr_t>(workspace) & 15) | (reinterpret_cast<uintptr_t>(out) & 7)) == 0,
+              "w4a16_moe: workspace must be 16-byte and out 8-byte aligned");
   MoeParams p{};
   p.hidden = static_cast<const uint16_t*>(hidden);
   p.T = (int)T;
@@ -732,7 +744,7 @@ extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I
   const size_t max_rows = max_padded_rows(T * topk, E);
   const size_t hb = ((max_rows * I * 2 + 255) / 256) * 256;
   p.hbuf = static_cast<uint16_t*>(workspace);
-  p.ypair = reinterpret_cast<float*>(static_cast<char*>(workspace) + hb);
+  p.ypair = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + hb);
   p.out = static_cast<uint16_t*>(out);
   const unsigned tiles = (unsigned)((max_rows + kTile - 1) / kTile);
   hipStream_t st = (hipStream_t)stream;
@@ -747,7 +759,7 @@ extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I
   launch_experts(p, gu_zero != nullptr, sz_dtype, gu_grid, dn_grid, gu_chunk, dn_chunk, gu_lds, dn_lds, st);
   int rc = check_launch("w4a16_moe experts");
   if (rc) return rc;
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)T), dim3(256), 0, st,
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T), dim3(256), 0, st,
                      p.ypair, (int)topk, (int)H, p.out);
   return check_launch("w4a16_moe combine");
 }
