@@ -83,20 +83,22 @@ wo_tile_kernel(TileParams p) {
   const int u0 = p.units * wv / W, u1 = p.units * (wv + 1) / W;
   const int st0 = u0 * p.unit_steps, nst = (u1 - u0) * p.unit_steps;
 
-  // ---- activation loads first (the whole K for M rows), round 0 into registers
-  const int xcols = p.steps * (kStepK / 8);  // 16-byte pieces per activation row
-  const int npieces = M * xcols;
+  // ---- activation loads first: each wavefront stages the M rows of its own slice of K
+  // (the slices do not overlap, so no barrier is needed before the multiply), round 0
+  // into registers
+  const int scols = nst * (kStepK / 8);  // 16-byte pieces per activation row in the slice
+  const int npieces = M * scols;
   const int xld = (int)(p.ldx / 8);
   const uint4* xsrc = reinterpret_cast<const uint4*>(p.x);
   uint4 xr[XP];
-  // rounds of XP pieces per thread; pieces j of a round that no thread needs are not
-  // loaded (a uniform branch)
+  // rounds of XP x 64 pieces; pieces j of a round past the slice are not loaded (a
+  // uniform branch). Piece i: row i / scols, column st0 * 16 + i % scols.
   auto load_x = [&](int base) {
 #pragma unroll
     for (int j = 0; j < XP; ++j) {
-      if (base + j * kThreads + wv * 64 < npieces) {  // this wavefront has pieces
-        const int i = min(base + tid + j * kThreads, npieces - 1);
-        const int m = i / xcols, c = i - m * xcols;
+      if (base + j * 64 < npieces) {
+        const int i = min(base + lane + j * 64, npieces - 1);
+        const int m = i / scols, c = st0 * (kStepK / 8) + i - m * scols;
         xr[j] = xsrc[(int64_t)m * xld + c];
       }
     }
@@ -181,14 +183,14 @@ wo_tile_kernel(TileParams p) {
   constexpr float kXBias = KIND == KIND_INT4 && !HZ ? -136.f : -128.f;
   const int xstride = p.steps * kStepK + 8;
   float* xsum = reinterpret_cast<float*>(lds + M * xstride);
-  for (int base = 0; base < npieces; base += XP * kThreads) {
+  for (int base = 0; base < npieces; base += XP * 64) {
     if (base != 0) load_x(base);
 #pragma unroll
     for (int j = 0; j < XP; ++j) {
-      if (base + j * kThreads + wv * 64 >= npieces) break;  // no pieces loaded for this wavefront
-      const int i = base + tid + j * kThreads;
+      if (base + j * 64 >= npieces) break;  // past the slice
+      const int i = base + lane + j * 64;
       const int ic = min(i, npieces - 1);
-      const int m = ic / xcols, c = ic - m * xcols;
+      const int m = ic / scols, c = st0 * (kStepK / 8) + ic - m * scols;
       *reinterpret_cast<uint4*>(lds + m * xstride + c * 8) = KIND == KIND_INT4 ? permute_for_u4(xr[j]) : xr[j];
       // 16 consecutive lanes (one DPP row) hold the 16 pieces of one k-step of one row
       float sm = sum8_bf16(xr[j]);
@@ -199,7 +201,10 @@ wo_tile_kernel(TileParams p) {
       if (i < npieces && (c & 15) == 15) xsum[(c >> 4) * 16 + m] = sm * kXBias;
     }
   }
-  __syncthreads();
+  // this wavefront's LDS writes are complete before its lanes read each other's
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_wave_barrier();
   MIQ_TRACE(2);
 
   // ---- multiply the slice. Per quantization group, T = sum_k x (128 + u) + kXBias * sum_k x
