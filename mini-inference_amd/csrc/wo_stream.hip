@@ -32,6 +32,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "wo_core.h"
 
@@ -443,14 +444,19 @@ wo_stream_kernel(StreamParams p_in) {
   __syncthreads();
   MIQ_TRACE(6);
   if (!s_last) return;
-  // 4 consecutive n per thread and round; the S partials of 4 such vectors are requested
-  // 4 splits at a time with agent-coherent (sc1) 16-byte loads, then added in split order
+  // 4 consecutive n per thread and round; the S partials of VB such vectors are
+  // requested SU splits at a time (VB * SU = 16 loads in flight) with agent-coherent (sc1)
+  // 16-byte loads, then added in split order (a missing split adds zeros). VB is the most
+  // vectors a thread can have (at most 4 per round).
   constexpr int kRows = kWaves * NR * 16;
-  constexpr int VB = 4;
+  constexpr int kMaxVec = MT * 16 * (kRows / 4);
+  constexpr int VB = (kMaxVec + kThreads - 1) / kThreads < 4 ? (kMaxVec + kThreads - 1) / kThreads : 4;
+  constexpr int SU = 16 / VB;
   const __amdgpu_buffer_rsrc_t prs =
       __builtin_amdgcn_make_buffer_rsrc(p.partial, 0, (int)((int64_t)p.S * M * p.N * 4), 0x00020000);
   const int nvec = M * (kRows / 4);
-  for (int v0 = tid; v0 < nvec; v0 += kThreads * VB) {
+  for (int b0 = 0; b0 < nvec; b0 += kThreads * VB) {
+    const int v0 = b0 + tid;
     float4 o[VB];
     int off[VB];
     bool ok[VB];
@@ -463,18 +469,24 @@ wo_stream_kernel(StreamParams p_in) {
       o[j] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     const int sstride = M * p.N * 4;
-    for (int s0 = 0; s0 < p.S; s0 += 4) {
-      float4 t[4][VB];
+    // SU splits per round; 4 when there are at most 4 (fewer requests that go nowhere)
+    auto rounds = [&](auto su_c) {
+      constexpr int SUR = decltype(su_c)::value;
+      for (int s0 = 0; s0 < p.S; s0 += SUR) {
+        float4 t[SUR][VB];
+        // requests past the last split or vector go to an offset outside the buffer
+        // (zeros, no memory access): straight-line code, so the waits stay exact
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+        for (int j = 0; j < VB; ++j)
 #pragma unroll
-        for (int j = 0; j < VB; ++j) {
-          const auto w = __builtin_amdgcn_raw_buffer_load_b128(prs, off[j] + min(s0 + u, p.S - 1) * sstride, 0, 16 /* sc1 */);
-          t[u][j] = *reinterpret_cast<const float4*>(&w);
-        }
+          for (int u = 0; u < SUR; ++u) {
+            const bool live = s0 + u < p.S && b0 + j * kThreads < nvec;
+            const auto w = __builtin_amdgcn_raw_buffer_load_b128(prs, live ? off[j] + (s0 + u) * sstride : 0x7ffffff0,
+                                                                 0, 16 /* sc1 */);
+            t[u][j] = *reinterpret_cast<const float4*>(&w);
+          }
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (s0 + u < p.S)
+        for (int u = 0; u < SUR; ++u)
 #pragma unroll
           for (int j = 0; j < VB; ++j) {
             o[j].x += t[u][j].x;
@@ -482,7 +494,10 @@ wo_stream_kernel(StreamParams p_in) {
             o[j].z += t[u][j].z;
             o[j].w += t[u][j].w;
           }
-    }
+      }
+    };
+    if (SU > 4 && p.S <= 4) rounds(std::integral_constant<int, 4>{});
+    else rounds(std::integral_constant<int, SU>{});
 #pragma unroll
     for (int j = 0; j < VB; ++j) {
       if (!ok[j]) continue;
