@@ -46,9 +46,11 @@ using namespace wo;
 constexpr int kTileNS = 8;                 // k-steps in flight per wavefront (all of its slice)
 constexpr int kTileLds = 160 * 1024;       // gfx950 LDS per workgroup
 constexpr int kCUs = 256;                  // MI355X compute units
-// activation pieces (16 B) per thread per round (int8 holds twice the weight registers)
+// activation pieces (16 B) per lane per round (int8 holds twice the weight registers):
+// 12 x 64 pieces cover a wavefront's slice at M = 8 (8 rows x 6 k-steps) in one round;
+// 16 measured slower (register pressure)
 template <int KIND>
-constexpr int tile_xp() { return KIND == KIND_INT4 ? 8 : 4; }
+constexpr int tile_xp() { return KIND == KIND_INT4 ? 12 : 4; }
 
 struct TileParams {
   const uint16_t* x;
