@@ -12,10 +12,13 @@
 //     gives sum_k x over every k-step, which removes the +128 code offset (below) with 4
 //     FMAs per group instead of one MFMA per operand;
 //   * weights stream through a ring of D k-steps of registers: step k + D is requested
-//     (16-byte non-temporal buffer loads, one per lane) right after step k has been
-//     multiplied, so D steps are always in flight and the wait before a step is a
-//     constant count. Requests past the range use an offset outside the buffer, which
-//     the hardware answers with zeros without touching memory;
+//     (16-byte buffer loads, one per lane; non-temporal except in the M split) right
+//     after step k has been multiplied, so D steps are always in flight and the wait
+//     before a step is a constant count. Requests past the range use an offset outside
+//     the buffer, which the hardware answers with zeros without touching memory;
+//   * M split (int4, M > 16): grid.z runs over the 16-row activation tiles, each
+//     workgroup taking one of them with two weight tiles per wavefront; the workgroups of
+//     one row block on different activation tiles read the same weight lines (same XCD);
 //   * the code is a pair of short loops: these kernels run for a few microseconds, and
 //     the instruction fetch of straight-line code costs about as much as the loads;
 //   * with S > 1 every workgroup publishes fp32 partials with agent-coherent (sc1)
@@ -24,10 +27,13 @@
 //
 // Unpacking: a 4-bit code u becomes the bf16 value 128 + u with one AND-OR per pair
 // (0x4300 | u == 128 + u, exact) and an int8 code q becomes 128 + q via xor + byte
-// convert. The MFMA yields sum x * (128 + u); then per group (int4)
-//   acc += scale * sum x (128 + u) + (zero - 128 scale) * sum x     (asymmetric)
-//   acc += scale * sum x (128 + u) - 136 scale * sum x              (symmetric, u - 8)
+// convert. The MFMA yields sum x * (128 + u); the staged sums hold bias * sum x (bias
+// -136 for symmetric int4 codes u - 8, -128 with zero points and for int8), and per
+// group (int4)
+//   acc += scale * (sum x (128 + u) + bias * sum x)  [+ zero * sum x with zero points]
 // and per row (int8) y = bf16(bf16(sum x (128 + q) - 128 sum x) * bf16(scale)).
+// One-step (128-code) int4 groups have their own instantiation (G1): each k-step's
+// MFMA chains start from its bias sums and from zero, and end the group at once.
 #include <stdio.h>
 #include <stdlib.h>
 
@@ -40,8 +46,8 @@
 #define MIQ_TRACE(point)
 #endif
 
-// ring depth (k-steps of int4 weights in flight per wavefront) for one activation tile;
-// 8 and 16 measured the same or 8 slightly better on the decode shapes
+// ring depth (k-steps of int4 weights in flight per wavefront, divided by NR) for one
+// activation tile; 8 and 16 measured slower on MI355X (their registers cost occupancy)
 #ifndef MIQ_D1
 #define MIQ_D1 4
 #endif

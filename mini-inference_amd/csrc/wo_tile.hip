@@ -3,23 +3,23 @@
 //
 //   y[m, n] = sum_k x[m, k] * W[n, k],  x bf16 [M, K],  W int8 [N, K] or int4 [N, K/2]
 //
-// A workgroup of W wavefronts owns one tile of 16 weight rows over the whole K; the K
-// range is cut into W slices of whole quantization groups, one per wavefront. Every
-// wavefront requests its whole slice of weights (at most 8 k-steps, 8 KiB) and scales at
-// once, right after the activation loads, so a wavefront sees one memory round trip
-// instead of a ring of them. The activations (all of K) are staged in LDS once per
-// workgroup; the W partial tiles are added through LDS in wavefront order, so there is
-// no split-K workspace, no cross-workgroup counter and no second round trip for partial
-// sums. A tile holds R <= 16 weight rows (the MFMA tile's other rows read nothing and
-// are not written): a launch has N / R workgroups of 4 to 16 wavefronts, R chosen so that
-// the workgroups cover every CU. One CU streams at a limited rate whatever the load on the
-// rest of the chip (on MI355X an M=1 tile of 16 x 9728 int4 weights takes as long with 80
-// workgroups in the launch as with 256), so the bytes per CU set the time.
+// A workgroup of W wavefronts owns one tile of R <= 16 weight rows over the whole K (the
+// MFMA tile's other rows read nothing and are not written); a launch has N / R
+// workgroups of 4 to 16 wavefronts, R chosen so that the workgroups cover every CU. The
+// K range is cut into W slices of whole quantization groups, one per wavefront. Every
+// wavefront requests its slice's activations, then its whole slice of weights (at most 8
+// k-steps) and scales at once, so it sees one memory round trip instead of a ring of
+// them. Each wavefront stages the activations of its own slice in LDS (the slices do not
+// overlap, so no workgroup barrier precedes the multiply); the W partial tiles are added
+// through LDS in wavefront order, so there is no split-K workspace, no cross-workgroup
+// counter and no second round trip for partial sums. At M = 1 the time follows the
+// k-steps per wavefront rather than the bytes per CU (on MI355X an M=1 launch takes about
+// as long with 80 workgroups as with 256; halving K saves a third).
 //
 // Per-element math is the one of the streamed kernel (wo_stream.hip): codes unpack to
-// bf16 128 + code, MFMA 16x16x32 bf16 with fp32 accumulation in two chains, per-group
-// scales applied as acc += s * accg + (z - 128 s) * sum(x) (int4; -136 s for symmetric
-// codes) and acc - 128 * sum(x) then the row scale for int8.
+// bf16 128 + code, MFMA 16x16x32 bf16 with fp32 accumulation, and per quantization group
+// acc += s * (sum x (128 + code) + bias * sum x) (bias -136 for symmetric int4 codes, -128
+// with zero points, plus z * sum x); int8: acc - 128 * sum x, then the row scale.
 //
 // Weight loads read whole 128-byte lines: load h of the tile covers its rows 8h .. 8h + 7,
 // 128 bytes each (two int4 k-steps or one int8 k-step), with four consecutive lanes on 64
