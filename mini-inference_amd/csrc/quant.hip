@@ -137,16 +137,21 @@ fp8_quantize_rows_kernel(const void* __restrict__ x, int x_dtype, int64_t K, int
     for (int64_t c = threadIdx.x; c < K / 8; c += blockDim.x) {
       const uint4 p = xv[c];
       const uint32_t d[4] = {p.x, p.y, p.z, p.w};
-      uint32_t o[2] = {0, 0};
+      // the hardware e4m3 (OCP) conversion rounds to nearest even like f32_to_fp8; the
+      // inputs are clamped to +-448 first, as the reference does
+      int o[2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float a = fminf(fmaxf(bf16_to_f32(d[i] & 0xffff) / s, -448.f), 448.f);
-        const float b = fminf(fmaxf(bf16_to_f32(d[i] >> 16) / s, -448.f), 448.f);
-        const uint32_t pair = static_cast<uint32_t>(f32_to_fp8(a)) |
-                              (static_cast<uint32_t>(f32_to_fp8(b)) << 8);
-        o[i >> 1] |= pair << (16 * (i & 1));
+      for (int h = 0; h < 2; ++h) {
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          v[2 * i] = fminf(fmaxf(bf16_to_f32(d[2 * h + i] & 0xffff) / s, -448.f), 448.f);
+          v[2 * i + 1] = fminf(fmaxf(bf16_to_f32(d[2 * h + i] >> 16) / s, -448.f), 448.f);
+        }
+        o[h] = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+        o[h] = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], o[h], true);
       }
-      qv[c] = make_uint2(o[0], o[1]);
+      qv[c] = make_uint2((uint32_t)o[0], (uint32_t)o[1]);
     }
     if (threadIdx.x == 0) scale[row] = s;
     return;

@@ -95,6 +95,25 @@ def test_fp8_codec_known_answers_and_all_codes():
     assert same_bytes(q, row.to(torch.float8_e4m3fn))
 
 
+def test_fp8_quantize_rows_every_bf16_value():
+    """The bf16 path's e4m3 encode on every bf16 value in [-448, 448] (a row with amax 448,
+    so the scale is 1 and each code is the encode of the value itself): every normal and
+    subnormal e4m3 code, every tie between neighbours, against the oracle's restated
+    encode and torch's float8_e4m3fn conversion."""
+    from kernels import quant_ops as ops
+    case("fp8 rows every bf16 value")
+    bits = torch.arange(1 << 16, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    vals = bits[~torch.isnan(bits.float())]
+    vals = vals[vals.float().abs() <= 448.0]
+    row = torch.cat([vals, torch.tensor([448.0], dtype=torch.bfloat16)])
+    row = torch.cat([row, torch.zeros((-row.numel()) % 8, dtype=torch.bfloat16)]).reshape(1, -1)
+    q, s = ops.fp8_quantize_rows(row.to(DEV))
+    assert s.item() == 1.0
+    want = O.fp8_quantize(row)
+    assert same_bytes(q, want["qweight"])
+    assert same_bytes(q, row.float().to(torch.float8_e4m3fn))
+
+
 @pytest.mark.parametrize("kind", ["int8", "fp8"])
 def test_kv_quant_write_bit_exact(kind):
     from engine.core.kv_cache import KVCache
