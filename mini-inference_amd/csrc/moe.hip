@@ -348,7 +348,10 @@ moe_down_kernel(MoeParams p, int chunk_steps) {
 //   down (DN):    wavefront w owns H rows 128 b + 32 w .. + 31 (two tiles); the product
 //                 times the routing weight goes to ypair[pair]
 enum { MOE_GU = 0, MOE_DN = 1 };
-constexpr int kMoeD = 8;       // ring depth (k-steps; 16 measured slower)
+// ring depth in k-steps: one pair of k-steps per weight tile in flight. On MI355X at the
+// OLMoE layer the layer took 69.5-70.3 us with 2, 70.3-71.1 with 4, 74-75 with 6 and
+// 77-78 with 8 (16 slower still): fewer loads in flight per wavefront is faster here
+constexpr int kMoeD = 2;
 constexpr int kMoeChunk = 16;  // k-steps of activations staged at once
 #ifndef MIQ_MOE_RUN
 #define MIQ_MOE_RUN 2
