@@ -751,14 +751,17 @@ void launch_split3(const AttnParams& p, dim3 grid, hipStream_t st) {
     // pipelined over two register sets (256, the default, measured fastest on MI355X; a
     // 4-chunk pipeline needs more than 256 VGPRs); any other partition: 4 wavefronts,
     // chunk after chunk
-    // 16-token pages (the reference's block size) take the scalar page-id path
+    // 16-token pages (the reference's block size) take the scalar page-id path; with
+    // 256-token partitions that path runs 4 wavefronts of 2 chunks of 32 tokens (143.7
+    // against 146.0-146.3 us at the Qwen3 decode shape on MI355X; 2 wavefronts of 4 chunks
+    // of 32 measured the same as 2 of 2 x 64, one chunk of 128 per wavefront 10 % slower)
     const bool p16 = p.page == 16;
     if (p.partition == 512 && p16)
       hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 4, true>), grid, dim3(4 * 64), 0, st, p);
     else if (p.partition == 512)
       hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 4>), grid, dim3(4 * 64), 0, st, p);
     else if (p.partition == 256 && p16)
-      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 2, true>), grid, dim3(2 * 64), 0, st, p);
+      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 1, 2, 4, true>), grid, dim3(4 * 64), 0, st, p);
     else if (p.partition == 256)
       hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 2>), grid, dim3(2 * 64), 0, st, p);
     else if (p.partition == 128 && p16)
