@@ -66,7 +66,8 @@ def test_int4_symmetric_quantize_dequantize_bit_exact(shape, group):
 
 
 @pytest.mark.parametrize("shape,dtype,std", [((64, 256), torch.bfloat16, 0.02), ((2048, 2560), torch.bfloat16, 1.0),
-                                             ((6144, 2560), torch.float32, 0.02), ((7, 200), torch.bfloat16, 3.0)])
+                                             ((6144, 2560), torch.float32, 0.02), ((7, 200), torch.bfloat16, 3.0),
+                                             ((5, 8192), torch.bfloat16, 1.0), ((3, 8200), torch.bfloat16, 1.0)])
 def test_fp8_quantize_rows_bit_exact(shape, dtype, std):
     from kernels import quant_ops as ops
     case(f"fp8 rows {shape} {dtype}")
