@@ -751,13 +751,15 @@ void launch_split3(const AttnParams& p, dim3 grid, hipStream_t st) {
     // pipelined over two register sets (256, the default, measured fastest on MI355X; a
     // 4-chunk pipeline needs more than 256 VGPRs); any other partition: 4 wavefronts,
     // chunk after chunk
-    // 16-token pages (the reference's block size) take the scalar page-id path; with
-    // 256-token partitions that path runs 4 wavefronts of 2 chunks of 32 tokens (143.7
-    // against 146.0-146.3 us at the Qwen3 decode shape on MI355X; 2 wavefronts of 4 chunks
-    // of 32 measured the same as 2 of 2 x 64, one chunk of 128 per wavefront 10 % slower)
+    // 16-token pages (the reference's block size) take the scalar page-id path, whose
+    // wavefronts each run 2 chunks of 32 tokens (2 / 4 / 8 wavefronts for 128 / 256 / 512-
+    // token partitions). At the Qwen3 decode shape on MI355X: 256 143.7 against 146.0-146.3
+    // us with 2 chunks of 64 (2 wavefronts of 4 chunks of 32 the same as 2 of 2 x 64, one
+    // chunk of 128 per wavefront 10 % slower); 512 143-144 against 150-151; 128 149-150
+    // against 151.5-152
     const bool p16 = p.page == 16;
     if (p.partition == 512 && p16)
-      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 4, true>), grid, dim3(4 * 64), 0, st, p);
+      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 1, 2, 8, true>), grid, dim3(8 * 64), 0, st, p);
     else if (p.partition == 512)
       hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 4>), grid, dim3(4 * 64), 0, st, p);
     else if (p.partition == 256 && p16)
@@ -765,7 +767,7 @@ void launch_split3(const AttnParams& p, dim3 grid, hipStream_t st) {
     else if (p.partition == 256)
       hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 2>), grid, dim3(2 * 64), 0, st, p);
     else if (p.partition == 128 && p16)
-      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 1, true>), grid, dim3(1 * 64), 0, st, p);
+      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 1, 2, 2, true>), grid, dim3(2 * 64), 0, st, p);
     else if (p.partition == 128)
       hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 1>), grid, dim3(1 * 64), 0, st, p);
     else
