@@ -15,6 +15,7 @@ _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.environ.get("MIQ_LIB", os.path.join(_PKG_DIR, "libmiq.so"))
 
 MIQ_F32, MIQ_BF16, MIQ_F16, MIQ_FP8_E4M3, MIQ_INT8, MIQ_UINT8, MIQ_INT32, MIQ_INT64 = range(8)
+ABI_VERSION = 1  # miq_abi_version() of the library these signatures describe
 
 _DTYPE_CODES = {
     torch.float32: MIQ_F32,
@@ -73,6 +74,10 @@ def load():
                 fn = getattr(lib, name)
                 fn.restype = res
                 fn.argtypes = args
+            version = lib.miq_abi_version()
+            if version != ABI_VERSION:
+                raise RuntimeError(f"{LIB_PATH} has ABI version {version}, this binding expects {ABI_VERSION}; "
+                                   f"rebuild the library")
             _lib = lib
     return _lib
 
