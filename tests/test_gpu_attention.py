@@ -96,13 +96,14 @@ def test_partitions_agree():
 @pytest.mark.parametrize("partition,lens", [(None, [40, 7, 90]), (128, [600, 7, 1290, 300]),
                                             (256, [600, 7, 1290, 300]), (384, [600, 7, 1290]),
                                             (512, [600, 7, 1290, 1100])])
-def test_quantized_cache_written_by_kvcache(kind, partition, lens):
+@pytest.mark.parametrize("H,KV", [(4, 4), (32, 2)])
+def test_quantized_cache_written_by_kvcache(kind, partition, lens, H, KV):
     """reference tests/test_paged_attention.py:73-89 with the HIP quantize-on-write; every
     partition size with its own kernel instance (128, 256, 512) and the generic one (384),
-    with requests that end inside a chunk, a partition, or after one token."""
+    with requests that end inside a chunk, a partition, or after one token; one kv head per
+    q head, and the largest group the kernels take (16 q heads per kv head)."""
     from engine.core.kv_cache import KVCache
-    case(f"quantized cache {kind} partition {partition} lens {lens}")
-    H = KV = 4
+    case(f"quantized cache {kind} partition {partition} lens {lens} H={H} KV={KV}")
     D, page = 128, 16
     q, k, v, t, sl = random_paged(lens, H, KV, D, page, seed=2)
     cache = KVCache("paged", 1, KV, D, k.shape[0] + 16, torch.bfloat16, DEV, block_size=page, kv_dtype=kind)
