@@ -2,8 +2,10 @@
 //
 // Work decomposition: one workgroup per (partition of `partition` tokens, kv head,
 // request). All GROUP = H / KV query heads of the kv head are handled together, so every
-// K/V byte is read from HBM once (not once per query head). The four wavefronts of a
-// workgroup take consecutive quarters of the partition and walk it 32 tokens at a time:
+// K/V byte is read from HBM once (not once per query head). The wavefronts of a workgroup
+// (four for bf16 caches; for 8-bit caches one to eight by partition size and page size,
+// see launch_split3) take consecutive slices of the partition and walk them 32 tokens at a
+// time:
 //
 //   scores  S[h, t] = q[h] . K[t]      v_mfma_f32_16x16x32_bf16, A = q (rows = heads,
 //                                       zero-padded to 16), B = K^T (columns = tokens);
