@@ -42,6 +42,12 @@ enum miq_dtype {
 const char* miq_last_error(void);
 int miq_abi_version(void);
 
+/* Re-reads the MIQ_* kernel-selection variables (MIQ_WO_STREAM, MIQ_WO_PANEL, ...), which
+ * the library otherwise reads once when it is loaded. No counterpart in the reference: a
+ * hook for tests and tuning runs that switch kernels inside one process. Not to be
+ * called while another thread launches kernels of this library. */
+int miq_tuning_reload(void);
+
 /* ------------------------------------------------------------------ weight quantization
  * Replaces Int8WeightOnly.quantize (engine/quantization/int8_wo.py:8-12):
  *   s = max|w_row| clamped to 1e-8, divided by 127 (fp32); q = round_half_even(w / s)
@@ -174,14 +180,18 @@ int miq_moe_align(const void* topk_ids, int idx_dtype, int64_t num_pairs, int64_
  * experts: out[t] = sum_j w[t,j] * down_e( silu(gate_e(x_t)) * up_e(x_t) ), e = ids[t,j].
  * hidden: bf16 [T, H]; gate_up q: uint8 [E, 2I, H/2], scale/zero [E, 2I, H/group];
  * down q: uint8 [E, H, I/2], scale/zero [E, H, I/group]; zero pointers may be NULL
- * (symmetric); topk_weights bf16 [T, k]; sorted_ids / expert_ids / num_padded from
- * miq_moe_align with block_m == 16. Workspace bytes from miq_moe_workspace_bytes.
- * out: bf16 [T, H]. */
+ * (symmetric); topk_weights [T, k] in w_dtype (f32 / bf16 / f16, k <= 32); sorted_ids /
+ * expert_ids / num_padded from miq_moe_align with block_m == 16. Workspace bytes from
+ * miq_moe_workspace_bytes. out: bf16 [T, H].
+ * Rounding follows the reference loop: gate/up and down outputs rounded to bf16, the
+ * product with the routing weight (in its own dtype) rounded to bf16, and a token's
+ * contributions added in ascending expert order with a bf16 rounding after each
+ * addition (index_add_ into a bf16 output). */
 size_t miq_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I);
 int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
                   const uint8_t* gu_q, const void* gu_scale, const void* gu_zero,
                   const uint8_t* dn_q, const void* dn_scale, const void* dn_zero,
-                  int sz_dtype, int64_t group, const void* topk_weights,
+                  int sz_dtype, int64_t group, const void* topk_weights, int w_dtype,
                   const int32_t* sorted_ids, const int32_t* expert_ids,
                   const int32_t* num_padded, void* workspace, size_t workspace_bytes,
                   void* out, void* stream);

@@ -1,10 +1,48 @@
-// Error reporting for the C ABI.
+// Error reporting for the C ABI, and the tuning switches read from the environment.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
+
+#include <mutex>
 
 #include "miq_common.h"
 
 namespace miq {
+
+namespace {
+Tuning read_tuning() {
+  Tuning t{};
+  auto flag = [](const char* name) { return getenv(name) != nullptr; };
+  auto pair = [](const char* name, int& a, int& b) {
+    const char* e = getenv(name);
+    return e && sscanf(e, "%d,%d", &a, &b) == 2;
+  };
+  t.wo_stream = flag("MIQ_WO_STREAM");
+  const char* rows = getenv("MIQ_WO_ROWS");
+  t.wo_rows = rows ? atoi(rows) : 0;
+  t.wo_msplit_set = pair("MIQ_WO_MSPLIT", t.wo_msplit_nr, t.wo_msplit_s);
+  t.wo_plan_set = pair("MIQ_WO_PLAN", t.wo_plan_nr, t.wo_plan_s);
+  const char* panel = getenv("MIQ_WO_PANEL");
+  t.wo_panel = panel ? atoi(panel) : -1;
+  const char* ps = getenv("MIQ_WO_PANEL_S");
+  t.wo_panel_s = ps ? atoi(ps) : 0;
+  const char* pm = getenv("MIQ_WO_PANEL_MT");
+  t.wo_panel_mt = pm ? atoi(pm) : 0;
+  const char* pa = getenv("MIQ_WO_PANEL_ABL");
+  t.wo_panel_abl = pa ? atoi(pa) : 0;
+  t.fp8_old = flag("MIQ_FP8_OLD");
+  const char* fw = getenv("MIQ_FP8_WAVES");
+  t.fp8_four_waves = fw && atoi(fw) == 4;
+  t.moe_tiled = flag("MIQ_MOE_TILED");
+  t.moe_align_scan = flag("MIQ_MOE_ALIGN_SCAN");
+  return t;
+}
+
+std::mutex g_tuning_lock;
+Tuning g_tuning = read_tuning();  // read once when the library is loaded
+}  // namespace
+
+const Tuning& tuning() { return g_tuning; }
 
 static thread_local char g_error[512] = "";
 
@@ -28,4 +66,10 @@ int check_launch(const char* what) {
 
 extern "C" const char* miq_last_error(void) { return miq::g_error; }
 
-extern "C" int miq_abi_version(void) { return 1; }
+extern "C" int miq_abi_version(void) { return 2; }
+
+extern "C" int miq_tuning_reload(void) {
+  std::lock_guard<std::mutex> hold(miq::g_tuning_lock);
+  miq::g_tuning = miq::read_tuning();
+  return MIQ_OK;
+}

@@ -16,6 +16,8 @@
 #include <cstdlib>
 #include <type_traits>
 
+#include <mutex>
+
 #include "miq_common.h"
 
 namespace miq {
@@ -166,12 +168,12 @@ int launch(const uint8_t* xq, const float* xs, const uint8_t* wq, const float* w
   using C = Fp8Cfg<BM, BN, WM, WN>;
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
   const int xcd = (tn % 8 == 0) ? 1 : 0;
-  static bool attr_set = false;
-  if (!attr_set) {
+  // the LDS limit is set once per kernel (thread-safe)
+  static std::once_flag lds_once;
+  std::call_once(lds_once, [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fp8_gemm_kernel<BM, BN, WM, WN>),
                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::kLds);
-    attr_set = true;
-  }
+  });
   hipLaunchKernelGGL((fp8_gemm_kernel<BM, BN, WM, WN>), dim3((unsigned)(tm * tn)), dim3(C::kThreads),
                      C::kLds, st, xq, xs, wq, ws, y, ldy, M, N, K, tm, tn, xcd);
   return check_launch("fp8_gemm");
@@ -412,12 +414,12 @@ int launch32w(const uint8_t* xq, const float* xs, const uint8_t* wq, const float
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
   const int xcd = (tn % 8 == 0) ? 1 : 0;
   constexpr size_t kLds = (size_t)kStages32 * (BM + BN) * BK32;
-  static bool attr_set = false;
-  if (!attr_set) {
+  // the LDS limit is set once per kernel (thread-safe)
+  static std::once_flag lds_once;
+  std::call_once(lds_once, [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&fp8_gemm32_kernel<BM, BN, WV>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLds);
-    attr_set = true;
-  }
+  });
   hipLaunchKernelGGL((fp8_gemm32_kernel<BM, BN, WV>), dim3((unsigned)(tm * tn)), dim3(WV * 64), kLds, st, xq, xs,
                      wq, ws, y, ldy, M, N, K, tm, tn, xcd);
   return check_launch("fp8_gemm");
@@ -429,7 +431,7 @@ int launch32(const uint8_t* xq, const float* xs, const uint8_t* wq, const float*
   // 8 wavefronts (two per SIMD, 64 x 96 each) measured 9 % faster than 4 of 128 x 96 on
   // MI355X (40 against 44 us at 2048 x 6144 x 2560): one wavefront's barrier and LDS
   // waits overlap the other's MFMAs. MIQ_FP8_WAVES=4 runs the 4-wavefront layout.
-  static const bool four = getenv("MIQ_FP8_WAVES") && atoi(getenv("MIQ_FP8_WAVES")) == 4;
+  const bool four = tuning().fp8_four_waves;
   if (four) return launch32w<BM, BN, 4>(xq, xs, wq, ws, y, ldy, M, N, K, st);
   return launch32w<BM, BN, 8>(xq, xs, wq, ws, y, ldy, M, N, K, st);
 }
@@ -453,7 +455,7 @@ extern "C" int miq_fp8_gemm(const uint8_t* xq, const float* x_scale, const uint8
   if (M >= 1024 && N % 192 == 0) {
     // the large-tile kernel addresses the operands through buffer descriptors (< 2 GiB)
     // and stores 16-byte pieces of y rows
-    if (!getenv("MIQ_FP8_OLD") && M * K < 0x7fffffffLL && N * K < 0x7fffffffLL && ldy % 8 == 0 &&
+    if (!tuning().fp8_old && M * K < 0x7fffffffLL && N * K < 0x7fffffffLL && ldy % 8 == 0 &&
         (reinterpret_cast<uintptr_t>(y) & 15) == 0)
       return launch32<256, 192>(xq, x_scale, wq, w_scale, yy, ldy, (int)M, (int)N, (int)K, st);
     return launch<256, 192, 4, 2>(xq, x_scale, wq, w_scale, yy, ldy, (int)M, (int)N, (int)K, st);

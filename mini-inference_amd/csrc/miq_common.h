@@ -169,6 +169,36 @@ __device__ inline float wave_sum(float v) {
 namespace miq {
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
+
+// Kernel-selection switches for tests and tuning, read from MIQ_* environment variables
+// once at load time (miq_tuning_reload re-reads them); the defaults are the measured best.
+struct Tuning {
+  bool wo_stream;             // MIQ_WO_STREAM: weight-only GEMMs take the streamed kernel
+  int wo_rows;                // MIQ_WO_ROWS: rows per tile of the tile kernel (0: default)
+  bool wo_msplit_set;         // MIQ_WO_MSPLIT="NR,S": M-split plan of the streamed kernel
+  int wo_msplit_nr, wo_msplit_s;
+  bool wo_plan_set;           // MIQ_WO_PLAN="NR,S": plan of the streamed kernel
+  int wo_plan_nr, wo_plan_s;
+  int wo_panel;               // MIQ_WO_PANEL: 0 off, 1 forced where it applies, -1 default
+  int wo_panel_s;             // MIQ_WO_PANEL_S: K splits of the panel kernel (0: planned)
+  int wo_panel_mt;            // MIQ_WO_PANEL_MT: activation tiles per panel workgroup (1, 2, 4)
+  int wo_panel_abl;           // MIQ_WO_PANEL_ABL: ablation runs (timing only; wrong results)
+  bool fp8_old;               // MIQ_FP8_OLD: the previous FP8 GEMM kernel family
+  bool fp8_four_waves;        // MIQ_FP8_WAVES=4
+  bool moe_tiled;             // MIQ_MOE_TILED: the tiled expert kernels
+  bool moe_align_scan;        // MIQ_MOE_ALIGN_SCAN: the one-wavefront-per-expert align
+};
+const Tuning& tuning();
+
+// Raises a kernel's dynamic LDS limit to what gfx950's 160 KiB leaves beside its static
+// LDS; call once per kernel (a rejected request would otherwise linger as the error the
+// next launch check reports, so any error of these calls is consumed here).
+inline void allow_max_dynamic_lds(const void* kernel) {
+  hipFuncAttributes a{};
+  if (hipFuncGetAttributes(&a, kernel) == hipSuccess)
+    (void)hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - (int)a.sharedSizeBytes);
+  (void)hipGetLastError();
+}
 }  // namespace miq
 
 #define MIQ_REQUIRE(cond, ...)                 \

@@ -16,6 +16,8 @@
 
 #include <algorithm>
 
+#include <mutex>
+
 #include "wo_core.h"
 
 namespace miq {
@@ -197,12 +199,14 @@ struct MoeParams {
   const void* dn_s;
   const void* dn_z;
   int sz_dtype, group_steps;
-  const uint16_t* topk_w;
+  const void* topk_w;   // routing weights [num_pairs], dtype w_dtype
+  int w_dtype;
   const int32_t* sorted_ids;
   const int32_t* expert_ids;
   const int32_t* num_padded;
   uint16_t* hbuf;  // [max_padded, I] bf16: silu(gate) * up per sorted row
   uint16_t* ypair;  // [num_pairs, H] bf16: routed down-projection per pair (bf16-rounded values)
+  int32_t* rank;    // [num_pairs]: position of the pair in sorted_ids (pairs of a lower expert first)
   uint16_t* out;   // [T, H]
 };
 
@@ -328,8 +332,9 @@ moe_down_kernel(MoeParams p, int chunk_steps) {
     const int m = g * 4 + v;
     const int pair = p.sorted_ids[tile * kTile + m];
     if (pair < p.num_pairs) {
-      const float w = bf16_to_f32(p.topk_w[pair]);
+      const float w = load_scalar(p.topk_w, p.w_dtype, pair);
       p.ypair[(int64_t)pair * p.H + n] = f32_to_bf16(bf16r(bf16r(acc[v]) * w));
+      if (blockIdx.x == 0 && wv == 0 && r == 0) p.rank[pair] = tile * kTile + m;
     }
   }
 }
@@ -581,8 +586,9 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
         const int m = g * 4 + v;
         const int pair = p.sorted_ids[tile * kTile + m];
         if (pair < p.num_pairs) {
-          const float w = bf16_to_f32(p.topk_w[pair]);
+          const float w = load_scalar(p.topk_w, p.w_dtype, pair);
           const int n0 = blk * 128 + wv * 32 + r;
+          if (blk == 0 && wv == 0 && r == 0) p.rank[pair] = tile * kTile + m;
           p.ypair[(int64_t)pair * p.H + n0] = f32_to_bf16(bf16r(bf16r(acc[0][v]) * w));
           p.ypair[(int64_t)pair * p.H + n0 + 16] = f32_to_bf16(bf16r(bf16r(acc[1][v]) * w));
         }
@@ -598,14 +604,12 @@ void launch_stream_experts_g(const MoeParams& p, int max_tiles, hipStream_t st) 
   const int bgu = p.I / 64, bdn = p.H / 128;
   (void)steps_gu;
   (void)steps_dn;
-  static bool attr = false;
-  if (!attr) {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_stream_kernel<MOE_GU, HZ, SD, G1>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_gu);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_stream_kernel<MOE_DN, HZ, SD, G1>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_gu);
-    attr = true;
-  }
+  // the LDS limit is set once per kernel (thread-safe)
+  static std::once_flag lds_once;
+  std::call_once(lds_once, [&] {
+    allow_max_dynamic_lds(reinterpret_cast<const void*>(&moe_stream_kernel<MOE_GU, HZ, SD, G1>));
+    allow_max_dynamic_lds(reinterpret_cast<const void*>(&moe_stream_kernel<MOE_DN, HZ, SD, G1>));
+  });
   // about two workgroups per CU, never more than the runs of items that could exist
   const int grid_gu = std::max(1, std::min(512, max_tiles * bgu / kItemsPerRun));
   const int grid_dn = std::max(1, std::min(512, max_tiles * bdn / kItemsPerRun));
@@ -620,20 +624,36 @@ void launch_stream_experts(const MoeParams& p, int max_tiles, hipStream_t st) {
   else launch_stream_experts_g<HZ, SD, false>(p, max_tiles, st);
 }
 
-// out[t][n] = sum over slots j (in order) of ypair[t * k + j][n] in fp32; four consecutive
-// n per thread (H is a multiple of 64)
-__global__ void moe_combine_kernel(const uint16_t* __restrict__ ypair, int topk, int H, uint16_t* __restrict__ out) {
+// out[t][n] = the sum of the token's pair outputs ypair[t * k + j][n] taken in the order of
+// their rank (ascending expert), rounded to bf16 after every addition: the reference adds
+// each expert's bf16 contribution into a bf16 output, expert after expert
+// (modules.py:55-75, index_add_). Four consecutive n per thread (H is a multiple of 64).
+constexpr int kMaxCombineK = 32;
+__global__ void moe_combine_kernel(const uint16_t* __restrict__ ypair, const int32_t* __restrict__ rank, int topk,
+                                   int H, uint16_t* __restrict__ out) {
   const int t = blockIdx.y;
   const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (n >= H) return;
+  // the slots of the token in rank order (k is small: a selection pass per slot)
+  int order[kMaxCombineK];
+  int last = -1;
+  for (int j = 0; j < topk; ++j) {
+    int best = -1, best_rank = 0x7fffffff;
+    for (int i = 0; i < topk; ++i) {
+      const int rk = rank[(int64_t)t * topk + i];
+      if (rk > last && rk < best_rank) { best_rank = rk; best = i; }
+    }
+    order[j] = best;
+    last = best_rank;
+  }
   float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
   const uint16_t* row = ypair + (int64_t)t * topk * H + n;
   for (int j = 0; j < topk; ++j) {
-    const uint2 v = *reinterpret_cast<const uint2*>(row + (int64_t)j * H);
-    s.x += __builtin_bit_cast(float, v.x << 16);
-    s.y += __builtin_bit_cast(float, v.x & 0xffff0000u);
-    s.z += __builtin_bit_cast(float, v.y << 16);
-    s.w += __builtin_bit_cast(float, v.y & 0xffff0000u);
+    const uint2 v = *reinterpret_cast<const uint2*>(row + (int64_t)order[j] * H);
+    s.x = bf16r(s.x + __builtin_bit_cast(float, v.x << 16));
+    s.y = bf16r(s.y + __builtin_bit_cast(float, v.x & 0xffff0000u));
+    s.z = bf16r(s.z + __builtin_bit_cast(float, v.y << 16));
+    s.w = bf16r(s.w + __builtin_bit_cast(float, v.y & 0xffff0000u));
   }
   const uint32_t lo = f32_to_bf16(s.x) | ((uint32_t)f32_to_bf16(s.y) << 16);
   const uint32_t hi = f32_to_bf16(s.z) | ((uint32_t)f32_to_bf16(s.w) << 16);
@@ -643,7 +663,7 @@ __global__ void moe_combine_kernel(const uint16_t* __restrict__ ypair, int topk,
 template <bool HZ, int SD>
 void launch_experts_t(const MoeParams& p, dim3 gu_grid, dim3 dn_grid, int gu_chunk, int dn_chunk, size_t gu_lds,
                       size_t dn_lds, hipStream_t st) {
-  if (p.H % 128 == 0 && p.I % 64 == 0 && !getenv("MIQ_MOE_TILED")) {
+  if (p.H % 128 == 0 && p.I % 64 == 0 && !tuning().moe_tiled) {
     launch_stream_experts<HZ, SD>(p, (int)gu_grid.y, st);
     return;
   }
@@ -684,7 +704,7 @@ extern "C" int miq_moe_align(const void* topk_ids, int idx_dtype, int64_t num_pa
   const int64_t max_blocks = (max_padded + block_m - 1) / block_m;
   const int64_t nch = (num_pairs + 63) / 64;
   const int64_t chunk_ints = 2 * E + 1 + nch * E + nch * 128;
-  if (chunk_ints * 4 <= 64 * 1024 && !getenv("MIQ_MOE_ALIGN_SCAN")) {
+  if (chunk_ints * 4 <= 64 * 1024 && !tuning().moe_align_scan) {
     hipLaunchKernelGGL(moe_align_chunks_kernel, dim3(1), dim3(1024), (size_t)chunk_ints * sizeof(int),
                        (hipStream_t)stream, topk_ids, idx_dtype, (int)num_pairs, (int)E, (int)block_m,
                        (int)max_padded, (int)max_blocks, sorted_ids, expert_ids, num_padded);
@@ -699,17 +719,20 @@ extern "C" int miq_moe_align(const void* topk_ids, int idx_dtype, int64_t num_pa
 
 extern "C" size_t miq_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I) {
   const size_t hb = max_padded_rows(T * topk, E) * (size_t)I * 2;
-  return ((hb + 255) / 256) * 256 + (size_t)T * topk * H * 2;
+  const size_t yb = (size_t)T * topk * H * 2;
+  return ((hb + 255) / 256) * 256 + ((yb + 255) / 256) * 256 + (size_t)T * topk * 4;
 }
 
 extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
                              const uint8_t* gu_q, const void* gu_scale, const void* gu_zero,
                              const uint8_t* dn_q, const void* dn_scale, const void* dn_zero,
-                             int sz_dtype, int64_t group, const void* topk_weights,
+                             int sz_dtype, int64_t group, const void* topk_weights, int w_dtype,
                              const int32_t* sorted_ids, const int32_t* expert_ids,
                              const int32_t* num_padded, void* workspace, size_t workspace_bytes,
                              void* out, void* stream) {
   MIQ_REQUIRE(sz_dtype == MIQ_F32 || sz_dtype == MIQ_BF16 || sz_dtype == MIQ_F16, "w4a16_moe: bad scale dtype");
+  MIQ_REQUIRE(w_dtype == MIQ_F32 || w_dtype == MIQ_BF16 || w_dtype == MIQ_F16, "w4a16_moe: bad routing weight dtype");
+  MIQ_REQUIRE(topk <= kMaxCombineK, "w4a16_moe: topk=%lld above %d", (long long)topk, kMaxCombineK);
   MIQ_REQUIRE(group >= kStepK && group % kStepK == 0 && H % group == 0 && I % group == 0,
               "w4a16_moe: group=%lld must be a multiple of 128 dividing H and I", (long long)group);
   MIQ_REQUIRE(H % 64 == 0 && I % 32 == 0 && T >= 1 && topk >= 1 && E >= 1 && H < (1 << 20) && I < (1 << 20),
@@ -740,7 +763,8 @@ extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I
   p.dn_z = dn_zero;
   p.sz_dtype = sz_dtype;
   p.group_steps = (int)(group / kStepK);
-  p.topk_w = static_cast<const uint16_t*>(topk_weights);
+  p.topk_w = topk_weights;
+  p.w_dtype = w_dtype;
   p.sorted_ids = sorted_ids;
   p.expert_ids = expert_ids;
   p.num_padded = num_padded;
@@ -748,6 +772,7 @@ extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I
   const size_t hb = ((max_rows * I * 2 + 255) / 256) * 256;
   p.hbuf = static_cast<uint16_t*>(workspace);
   p.ypair = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + hb);
+  p.rank = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + hb + (((size_t)T * topk * H * 2 + 255) / 256) * 256);
   p.out = static_cast<uint16_t*>(out);
   const unsigned tiles = (unsigned)((max_rows + kTile - 1) / kTile);
   hipStream_t st = (hipStream_t)stream;
@@ -763,6 +788,6 @@ extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I
   int rc = check_launch("w4a16_moe experts");
   if (rc) return rc;
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T), dim3(256), 0, st,
-                     p.ypair, (int)topk, (int)H, p.out);
+                     p.ypair, p.rank, (int)topk, (int)H, p.out);
   return check_launch("w4a16_moe combine");
 }

@@ -125,13 +125,37 @@ __device__ inline float sum16(float v) {
 // keeps results below 2^-126 normal (such weights are zero for this purpose)
 __device__ inline float exp2_le0(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Tokens one partition index covers for a request of L tokens: `partition`, or a multiple
+// of it when L does not fit max_parts partitions (a caller's max_len below the longest
+// context never cuts a request: its partitions grow instead).
+__device__ inline int partition_span(int L, int partition, int max_parts) {
+  const int64_t per = (int64_t)partition * max_parts;
+  const int k = L > per ? (int)((L + per - 1) / per) : 1;
+  return k * partition;
+}
+
+// An empty context (L = 0, e.g. a padded batch row): partition 0 of each head of the
+// group is an empty split (output 0, log-sum-exp -inf) and nothing is read.
+__device__ inline void write_empty_split(const AttnParams& p, int b, int kvh, int nthreads) {
+  for (int i = threadIdx.x; i < p.group * kD; i += nthreads) {
+    const int hh = i / kD, d = i % kD;
+    const int64_t base = ((int64_t)b * p.H + kvh * p.group + hh) * p.max_parts;
+    p.o_part[base * kD + d] = 0.f;
+    if (d == 0) p.lse_part[base] = -__builtin_inff();
+  }
+}
+
 template <int KVT, bool HAS_SCALE, int SD>
 __global__ void __launch_bounds__(kWaves * 64)
 paged_decode_split_kernel(AttnParams p) {
   const int part = blockIdx.y, kvh = blockIdx.x, b = blockIdx.z;  // kv heads of one partition are dispatched together (they share DRAM pages)
   const int L = p.lens[b];
-  const int p0 = part * p.partition;
-  if (part > 0 && p0 >= L) return;  // partition beyond this request's context
+  if (L <= 0) {
+    if (part == 0) write_empty_split(p, b, kvh, kWaves * 64);
+    return;
+  }
+  const int span = partition_span(L, p.partition, p.max_parts);
+  if (part * span >= L) return;  // partition beyond this request's context
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
   const int GROUP = p.group;
@@ -157,8 +181,6 @@ paged_decode_split_kernel(AttnParams p) {
   for (int i = lane; i < 16 * kPRow; i += 64) s_p[wv][i] = 0;
 
   const int per_wave = p.partition / kWaves;
-  const int t_begin = p0 + wv * per_wave;
-  const int t_end = min(t_begin + per_wave, L);
   const float qk_scale = p.sm_scale * kLog2e;
 
   float m_run[4], l_run[4];
@@ -173,6 +195,11 @@ paged_decode_split_kernel(AttnParams p) {
   uint16_t* vt = s_vt[wv];
   uint16_t* pp = s_p[wv];
 
+  // the span's partitions one after the other, the softmax state carried across them
+  const int span_end = min(part * span + span, L);
+  for (int p0 = part * span; p0 < span_end; p0 += p.partition) {
+  const int t_begin = p0 + wv * per_wave;
+  const int t_end = min(t_begin + per_wave, L);
   for (int t0 = t_begin; t0 < t_end; t0 += kStep) {
     // ---- K: lane handles token t0 + 16 * c + r, 32 d at g * 32
     float sc[2][4];
@@ -297,6 +324,7 @@ paged_decode_split_kernel(AttnParams p) {
     }
     wave_lds_sync();
   }
+  }
 
   // ---- merge the four wavefronts: heads 4 * g + v, d = 16 * j + r
 #pragma unroll
@@ -357,8 +385,12 @@ __global__ void __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2))
 paged_decode_split8_kernel(AttnParams p) {
   const int part = blockIdx.y, kvh = blockIdx.x, b = blockIdx.z;  // kv heads of one partition are dispatched together (they share DRAM pages)
   const int L = p.lens[b];
-  const int p0 = part * p.partition;
-  if (part > 0 && p0 >= L) return;  // partition beyond this request's context
+  if (L <= 0) {
+    if (part == 0) write_empty_split(p, b, kvh, W * 64);
+    return;
+  }
+  const int span = partition_span(L, p.partition, p.max_parts);
+  if (part * span >= L) return;  // partition beyond this request's context
   MIQ_TRACE(0);
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
@@ -389,8 +421,6 @@ paged_decode_split8_kernel(AttnParams p) {
   for (int i = lane; i < 16 * kPRowC; i += 64) s_p[wv][i] = 0;
 
   const int per_wave = p.partition / W;
-  const int t_begin = p0 + wv * per_wave;
-  const int t_end = min(t_begin + per_wave, L);
   const float qk_scale = p.sm_scale * kLog2e;
 
   float m_run[4], l_run[4];
@@ -402,6 +432,11 @@ paged_decode_split8_kernel(AttnParams p) {
 
   const int64_t head_off = (int64_t)kvh * p.kvs_h;
   const int32_t* btrow = p.bt + (int64_t)b * p.bt_stride;
+  // the span's partitions one after the other, the softmax state carried across them
+  const int span_end = min(part * span + span, L);
+  for (int p0 = part * span; p0 < span_end; p0 += p.partition) {
+  const int t_begin = p0 + wv * per_wave;
+  const int t_end = min(t_begin + per_wave, L);
   uint8_t* vl = s_v[wv];
   uint16_t* pp = s_p[wv];
   const int tq = (lane >> 3) * 4, dseg = (lane & 7) * 16;  // V: 4 tokens x 16 d per lane
@@ -413,6 +448,7 @@ paged_decode_split8_kernel(AttnParams p) {
   __shared__ int s_bt[kBtMax];
   const int pg0 = pshift >= 0 ? p0 >> pshift : p0 / page;
   if (NC > 0 && !P16) {
+    if (p0 != part * span) __syncthreads();  // every wavefront is done with the previous partition's entries
     const int pg1 = (min(p0 + p.partition, L) - 1 + page) / page;  // one past the last page in use
     for (int i = tid; i < pg1 - pg0; i += W * 64) s_bt[i] = btrow[pg0 + i];
     __syncthreads();
@@ -434,7 +470,7 @@ paged_decode_split8_kernel(AttnParams p) {
   constexpr int kWP = P16 ? NC * kPagesPerChunk : 1;
   int wpage[kWP];
   if constexpr (P16) {
-    const int wpg0 = t_begin >> 4, pg_last = (L - 1) >> 4;
+    const int wpg0 = t_begin >> 4, pg_last = (L - 1) >> 4;  // L >= 1 here
 #pragma unroll
     for (int j = 0; j < kWP; ++j) wpage[j] = btrow[min(wpg0 + j, pg_last)];
   }
@@ -653,6 +689,7 @@ paged_decode_split8_kernel(AttnParams p) {
       }
     }
   }
+  }  // partitions of the span
   MIQ_TRACE(3);
 
 #pragma unroll
@@ -706,9 +743,9 @@ paged_decode_merge_kernel(const float* __restrict__ o_part, const float* __restr
   __shared__ float s_w[kD];
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
   const int L = lens[b];
-  int np = (L + partition - 1) / partition;
+  const int span = partition_span(L, partition, max_parts);
+  int np = (L + span - 1) / span;  // <= max_parts by the choice of span
   if (np < 1) np = 1;
-  if (np > max_parts) np = max_parts;  // a context longer than the caller's max_len is cut
   const int64_t base = ((int64_t)b * H + h) * max_parts;
   float mx = -__builtin_inff(), den = 0.f, num = 0.f;
   for (int s0 = 0; s0 < np; s0 += kD) {  // kD partitions per round (one per thread)

@@ -4,6 +4,8 @@
 //
 // Argument checks live here. Up to 16 rows whose activations fit LDS run the one-tile-per-
 // workgroup kernel (wo_tile.hip); the rest the streamed split-K kernel (wo_stream.hip).
+#include <algorithm>
+
 #include "wo_core.h"
 
 namespace miq {
@@ -12,6 +14,12 @@ size_t wo_stream_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bit
 int wo_stream_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, const void* scale,
                      const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int M,
                      int N, int K, void* workspace, size_t ws_bytes, hipStream_t st, const char* name);
+size_t wo_panel_partial_bytes(int64_t M, int64_t N, int64_t K);
+int wo_panel_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, const void* scale,
+                    const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int M,
+                    int N, int K, void* workspace, size_t ws_bytes, size_t counter_bytes, hipStream_t st,
+                    const char* name, bool& launched);
+constexpr size_t kWoCounterBytes = 16384;  // the workspace's counter area (4096 ints)
 int wo_tile_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, const void* scale,
                    const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int M,
                    int N, int K, hipStream_t st, const char* name, bool& launched);
@@ -44,6 +52,12 @@ int run(int kind, const WoArgs& p, void* workspace, size_t ws_bytes, hipStream_t
   MIQ_REQUIRE((reinterpret_cast<uintptr_t>(p.w) & 15) == 0, "%s: weights must be 16-byte aligned", name);
   MIQ_REQUIRE(p.ldx >= p.K && p.ldy >= p.N, "%s: bad strides", name);
   bool launched = false;
+  if (kind == KIND_INT4) {
+    const int rc = wo_panel_launch(p.x, p.ldx, p.w, p.ldw, p.scale, p.zero, p.sz_dtype, p.group_steps, p.ngroups,
+                                   p.y, p.ldy, p.M, p.N, p.K, workspace, ws_bytes, kWoCounterBytes, st, name,
+                                   launched);
+    if (launched || rc != MIQ_OK) return rc;
+  }
   const int rc = wo_tile_launch(kind, p.x, p.ldx, p.w, p.ldw, p.scale, p.zero, p.sz_dtype, p.group_steps, p.ngroups,
                                 p.y, p.ldy, p.M, p.N, p.K, st, name, launched);
   if (launched || rc != MIQ_OK) return rc;
@@ -57,7 +71,9 @@ int run(int kind, const WoArgs& p, void* workspace, size_t ws_bytes, hipStream_t
 using namespace miq;
 
 extern "C" size_t miq_wo_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits) {
-  return wo_stream_workspace_bytes(M, N, K, weight_bits);
+  const size_t stream = wo_stream_workspace_bytes(M, N, K, weight_bits);
+  if (weight_bits != 4 || M < 1 || M > 64 || N < 1 || K < kStepK) return stream;
+  return std::max(stream, kWoCounterBytes + wo_panel_partial_bytes(M, N, K));
 }
 
 extern "C" int miq_w8a16_gemm(const void* x, int64_t ldx, const int8_t* q, const void* scale,

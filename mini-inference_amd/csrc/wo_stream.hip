@@ -23,7 +23,8 @@
 //     the instruction fetch of straight-line code costs about as much as the loads;
 //   * with S > 1 every workgroup publishes fp32 partials with agent-coherent (sc1)
 //     stores, waits for them and bumps a per-row-block arrival counter; the last one adds
-//     the S partials in split order (deterministic), writes bf16 and resets the counter.
+//     the S partials in split order (deterministic), writes bf16, sets the partials it
+//     read back to zero and resets the counter, so the workspace is all zeros between calls.
 //
 // Unpacking: a 4-bit code u becomes the bf16 value 128 + u with one AND-OR per pair
 // (0x4300 | u == 128 + u, exact) and an int8 code q becomes 128 + q via xor + byte
@@ -39,6 +40,8 @@
 
 #include <algorithm>
 #include <type_traits>
+
+#include <mutex>
 
 #include "wo_core.h"
 
@@ -487,9 +490,19 @@ wo_stream_kernel(StreamParams p_in) {
 #pragma unroll
           for (int u = 0; u < SUR; ++u) {
             const bool live = s0 + u < p.S && b0 + j * kThreads < nvec;
-            const auto w = __builtin_amdgcn_raw_buffer_load_b128(prs, live ? off[j] + (s0 + u) * sstride : 0x7ffffff0,
-                                                                 0, 16 /* sc1 */);
+            const int so = live ? off[j] + (s0 + u) * sstride : 0x7ffffff0;
+            const auto w = __builtin_amdgcn_raw_buffer_load_b128(prs, so, 0, 16 /* sc1 */);
             t[u][j] = *reinterpret_cast<const float4*>(&w);
+          }
+        // the partials go back to zero once read: the workspace holds zeros between calls
+        // (the panel kernel, which shares it, reads a non-zero word as a pending partial)
+        const i32x4 zero4 = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < VB; ++j)
+#pragma unroll
+          for (int u = 0; u < SUR; ++u) {
+            // only this thread's own vectors (clamped duplicates are read by their owner)
+            if (s0 + u < p.S && ok[j]) __builtin_amdgcn_raw_buffer_store_b128(zero4, prs, off[j] + (s0 + u) * sstride, 0, 16 /* sc1 */);
           }
 #pragma unroll
         for (int u = 0; u < SUR; ++u)
@@ -551,9 +564,9 @@ StreamPlan plan_stream(int kind, int64_t M, int64_t N, int64_t K, int group_step
   // the weights through L2, and each re-reads 16 activation rows instead of all M. For
   // int4 this measured up to 12 % faster on MI355X (int8 slower), best with about 480
   // workgroups. MIQ_WO_MSPLIT="NR,S" (NR 2 or 4) forces a plan, for tuning; "0,0" off.
-  const char* ms = getenv("MIQ_WO_MSPLIT");
-  int m_nr = 0, m_s = 0;
-  const bool m_env = ms && sscanf(ms, "%d,%d", &m_nr, &m_s) == 2;
+  const Tuning& tu = tuning();
+  int m_nr = tu.wo_msplit_nr, m_s = tu.wo_msplit_s;
+  const bool m_env = tu.wo_msplit_set;
   if (!m_env && kind == KIND_INT4 && M > 16) {
     m_nr = 2;
     const int64_t blocks2 = (N + 127) / 128, tiles = (M + 15) / 16;
@@ -566,9 +579,9 @@ StreamPlan plan_stream(int kind, int64_t M, int64_t N, int64_t K, int group_step
     S = m_s;
     M = 16;  // per workgroup
   }
-  const char* env = pl.mtiles > 1 ? nullptr : getenv("MIQ_WO_PLAN");  // "NR,S" override for tuning
-  int e_nr = 0, e_s = 0;
-  if (env && sscanf(env, "%d,%d", &e_nr, &e_s) == 2 && (e_nr == 1 || e_nr == 2) && e_s >= 1) {
+  const bool env = pl.mtiles == 1 && tu.wo_plan_set;  // "NR,S" override for tuning
+  const int e_nr = tu.wo_plan_nr, e_s = tu.wo_plan_s;
+  if (env && (e_nr == 1 || e_nr == 2) && e_s >= 1) {
     if (pl.MT >= 2 || e_nr == 1) pl.NR = e_nr;
     S = e_s;
   }
@@ -602,12 +615,12 @@ StreamPlan plan_stream(int kind, int64_t M, int64_t N, int64_t K, int group_step
 
 template <int KIND, bool HZ, int SD, int MT, int NR, bool G1>
 void launch_stream_g(const StreamParams& p, dim3 grid, size_t lds, hipStream_t st) {
-  static bool attr = false;
-  if (!attr) {
+  // the LDS limit is set once per kernel (thread-safe)
+  static std::once_flag lds_once;
+  std::call_once(lds_once, [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wo_stream_kernel<KIND, HZ, SD, MT, NR, G1>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBudget);
-    attr = true;
-  }
+  });
   hipLaunchKernelGGL((wo_stream_kernel<KIND, HZ, SD, MT, NR, G1>), grid, dim3(waves_for<MT>() * 64), lds, st, p);
 }
 

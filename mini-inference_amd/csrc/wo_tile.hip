@@ -30,6 +30,8 @@
 #include <algorithm>
 #include <cstdlib>
 
+#include <mutex>
+
 #include "miq_common.h"
 #include "wo_core.h"
 
@@ -316,12 +318,12 @@ wo_tile_kernel(TileParams p) {
 
 template <int KIND, bool HZ, int SD, int W, bool G1>
 void launch_tile_g(const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
-  static bool attr = false;
-  if (!attr) {
+  // the LDS limit is set once per kernel (thread-safe)
+  static std::once_flag lds_once;
+  std::call_once(lds_once, [&] {
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wo_tile_kernel<KIND, HZ, SD, W, G1>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, kTileLds);
-    attr = true;
-  }
+  });
   hipLaunchKernelGGL((wo_tile_kernel<KIND, HZ, SD, W, G1>), dim3(blocks), dim3(W * 64), lds, st, p);
 }
 
@@ -359,7 +361,7 @@ struct TilePlan {
 static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_steps) {
   TilePlan pl{0, 0, 0, 0, 0};
   if (M < 1 || M > 16 || N < 1 || K < kStepK) return pl;
-  if (getenv("MIQ_WO_STREAM")) return pl;  // force the streamed kernel (tuning, tests)
+  if (tuning().wo_stream) return pl;  // force the streamed kernel (tuning, tests)
   // int8 with more than 2 rows: the streamed kernel measured faster on MI355X (the staged
   // activations of a tile outweigh the saved round trips there)
   if (kind == KIND_INT8 && M > 2) return pl;
@@ -375,7 +377,7 @@ static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_s
   // N = 2560, K = 9728 on MI355X: M = 1 6.5 against 6.7 us with 10-row tiles, M = 8 10.7
   // against 11.1 us); before that change the 10-row tiles had been 4 % faster at M = 1.
   int rows = 16;
-  if (const char* e = getenv("MIQ_WO_ROWS")) rows = std::max(1, std::min(16, atoi(e)));
+  if (tuning().wo_rows > 0) rows = std::max(1, std::min(16, tuning().wo_rows));
   const int64_t tiles = (N + rows - 1) / rows;
   for (int W : {4, 8, 16}) {
     if ((units + W - 1) / W * us > kTileNS) continue;

@@ -13,11 +13,12 @@ METHODS = {
 
 
 def get_method(name: str, device="cpu", compute_dtype=torch.bfloat16, group_size=128, fp8_backend="auto"):
-    """Same factory as the reference (__init__.py:13-20)."""
-    if name not in METHODS:
-        raise ValueError(f"Unknown quantization '{name}'. Options: none, {', '.join(METHODS)}")
-    if name == "int4_wo":
-        return Int4WeightOnly(group_size=group_size, compute_dtype=compute_dtype)
-    if name == "fp8":
-        return FP8WeightAct(backend=fp8_backend, device=device, compute_dtype=compute_dtype)
-    return METHODS[name](compute_dtype=compute_dtype)
+    """Method object by registry name, with the reference factory's arguments and error
+    message (__init__.py:13-20): group_size goes to INT4, device and fp8_backend to FP8."""
+    try:
+        cls = METHODS[name]
+    except KeyError:
+        raise ValueError(f"Unknown quantization '{name}'. Options: none, {', '.join(METHODS)}") from None
+    extra = {"int4_wo": {"group_size": group_size},
+             "fp8": {"backend": fp8_backend, "device": device}}.get(name, {})
+    return cls(compute_dtype=compute_dtype, **extra)

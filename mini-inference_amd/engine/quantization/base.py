@@ -1,9 +1,11 @@
-"""QuantMethod interface (reference: engine/quantization/base.py:3-26).
+"""The quantization-method interface (reference: engine/quantization/base.py:3-26).
 
-Same names and contract as the reference: `quantize(w) -> dict`, `dequantize(**q)`,
-`linear(x, **q)`, `supports(w)`, `describe()`. The default `linear` is the reference's
-"dequantize then matmul" path (base.py:20-24); here the dequantize step is the HIP kernel
-and the matmul is the device GEMM of torch.
+A method turns a float weight into a dict of tensors (`quantize`), back into a float
+weight (`dequantize`), and multiplies activations by the stored form (`linear`).
+`supports` says whether a weight's shape fits the format; rejected weights stay in the
+model dtype. The generic `linear` rebuilds the float weight and calls an ordinary
+matmul (base.py:20-24); the subclasses replace it with the fused HIP kernels where the
+shapes allow.
 """
 import torch
 
@@ -12,11 +14,9 @@ class QuantMethod:
     name = "base"
 
     def __init__(self, compute_dtype=torch.bfloat16):
-        # dtype of activations and outputs
-        self.compute_dtype = compute_dtype
+        self.compute_dtype = compute_dtype  # activations in, outputs out
 
     def supports(self, weight: torch.Tensor) -> bool:
-        """Whether this weight's shape can be quantized (otherwise it stays in bf16)."""
         return True
 
     def quantize(self, weight: torch.Tensor) -> dict:
@@ -26,9 +26,8 @@ class QuantMethod:
         raise NotImplementedError
 
     def linear(self, x: torch.Tensor, **q) -> torch.Tensor:
-        """Rebuild the weight in x's dtype, then an ordinary matmul (base.py:20-24)."""
-        w = self.dequantize(**q).to(x.dtype)
-        return torch.nn.functional.linear(x, w)
+        """x @ dequantize(**q)^T with the weight cast to x's dtype first."""
+        return torch.nn.functional.linear(x, self.dequantize(**q).to(x.dtype))
 
     def describe(self) -> dict:
         return {"method": self.name}

@@ -31,6 +31,18 @@ class FP8WeightAct(QuantMethod):
         else:
             self.native = backend == "native"
 
+    def _padded_weight(self, qweight, pad):
+        """qweight with `pad` zero columns, made once per weight tensor instead of on every
+        call. The entry holds the source tensor, so its address cannot be reused by another
+        weight while the entry exists; an in-place update of the weight makes a new entry."""
+        key = (qweight.data_ptr(), qweight._version, tuple(qweight.shape))
+        cache = self.__dict__.setdefault("_pads", {})
+        hit = cache.get(key)
+        if hit is None or hit[0] is not qweight:
+            hit = (qweight, torch.nn.functional.pad(qweight.view(torch.uint8), (0, pad)).view(FP8))
+            cache[key] = hit
+        return hit[1]
+
     def supports(self, weight):
         """fp8.py:28-30."""
         return weight.shape[-1] % 16 == 0 and weight.shape[-2] % 16 == 0
@@ -61,7 +73,7 @@ class FP8WeightAct(QuantMethod):
             if K % 128:  # the MFMA kernel takes K in steps of 128: zero padding adds nothing
                 pad = 128 - K % 128
                 x_fp8 = torch.nn.functional.pad(x_fp8.view(torch.uint8), (0, pad)).view(FP8)
-                w = torch.nn.functional.pad(qweight.view(torch.uint8), (0, pad)).view(FP8)
+                w = self._padded_weight(qweight, pad)
             y = ops.fp8_gemm(x_fp8, x_scale, w, scale)
             return y.to(out_dtype).reshape(*x.shape[:-1], -1)
         # emulation (fp8.py:69-73): same FP8 rounding, matmul in the compute dtype

@@ -15,7 +15,7 @@ _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.environ.get("MIQ_LIB", os.path.join(_PKG_DIR, "libmiq.so"))
 
 MIQ_F32, MIQ_BF16, MIQ_F16, MIQ_FP8_E4M3, MIQ_INT8, MIQ_UINT8, MIQ_INT32, MIQ_INT64 = range(8)
-ABI_VERSION = 1  # miq_abi_version() of the library these signatures describe
+ABI_VERSION = 2  # miq_abi_version() of the library these signatures describe
 
 _DTYPE_CODES = {
     torch.float32: MIQ_F32,
@@ -34,6 +34,7 @@ _P, _I64, _I32, _F32, _SZ = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctype
 SIGNATURES = {
     "miq_last_error": (ctypes.c_char_p, []),
     "miq_abi_version": (_I32, []),
+    "miq_tuning_reload": (_I32, []),
     "miq_int8_quantize": (_I32, [_P, _I32, _I64, _I64, _I64, _P, _P, _I32, _P]),
     "miq_int8_dequantize": (_I32, [_P, _P, _I32, _I64, _I64, _P, _P]),
     "miq_int4_quantize": (_I32, [_P, _I32, _I64, _I64, _I64, _I64, _P, _P, _P, _I32, _P]),
@@ -52,7 +53,7 @@ SIGNATURES = {
     "miq_moe_align": (_I32, [_P, _I32, _I64, _I64, _I64, _P, _P, _P, _P]),
     "miq_moe_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "miq_w4a16_moe": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I32, _I64, _P,
-                             _P, _P, _P, _P, _SZ, _P, _P]),
+                             _I32, _P, _P, _P, _P, _SZ, _P, _P]),
 }
 
 _lib = None
@@ -112,14 +113,18 @@ def call(name, *args):
 
 
 # ---------------------------------------------------------------- workspaces
-# One zero-initialised buffer per device for the split-K counters / partials of the
-# weight-only GEMMs. Kernels leave the counters at zero, so it is reused as is; it only
-# grows (a new zeroed buffer) when a larger shape comes along.
+# Zero-initialised buffers for the split-K counters / partials of the weight-only GEMMs,
+# one per (device, stream): kernels leave the counters at zero, so a buffer is reused as
+# is by the launches of its stream, which run one after another. Two streams never share
+# one (concurrent launches would race on the counters). A buffer only grows (a new zeroed
+# buffer) when a larger shape comes along; the old one is released by the caching
+# allocator in the stream order of its last use.
 _wo_ws = {}
 
 
 def wo_workspace(device, nbytes):
-    key = (device.type, device.index)
+    st = torch.cuda.current_stream(device)
+    key = (device.type, device.index, st.cuda_stream)
     buf = _wo_ws.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)

@@ -45,7 +45,7 @@ def fused_moe_int4(hidden, topk_ids, topk_weights, gu_q, gu_scale, gu_zero, dn_q
         raise RuntimeError("fused_moe_int4: gate_up and down must share one group size")
     sorted_ids, expert_ids, num_padded = moe_align(topk_ids, E, BLOCK_M)
     h = hidden.contiguous()
-    w = topk_weights.to(torch.bfloat16).contiguous()
+    w = topk_weights.contiguous()  # used in its own dtype, as the reference multiplies by it
     nbytes = L.load().miq_moe_workspace_bytes(T, k, E, H, inter)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=hidden.device)
     out = torch.empty((T, H), dtype=torch.bfloat16, device=hidden.device)
@@ -55,6 +55,6 @@ def fused_moe_int4(hidden, topk_ids, topk_weights, gu_q, gu_scale, gu_zero, dn_q
            L.ptr(None if gu_zero is None else gu_zero.contiguous()),
            L.ptr(dn_q.contiguous()), L.ptr(dn_scale.contiguous()),
            L.ptr(None if dn_zero is None else dn_zero.contiguous()),
-           L.dtype_code(sdt), group, L.ptr(w), L.ptr(sorted_ids), L.ptr(expert_ids), L.ptr(num_padded),
+           L.dtype_code(sdt), group, L.ptr(w), L.dtype_code(w.dtype), L.ptr(sorted_ids), L.ptr(expert_ids), L.ptr(num_padded),
            L.ptr(ws), nbytes, L.ptr(out), L.stream(hidden.device))
     return out

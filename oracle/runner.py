@@ -55,7 +55,8 @@ class OracleLinear(nn.Module):
         super().__init__()
         self.name = qlinear.method.name
         self.dtype = dtype
-        self.q = {k: getattr(qlinear, k).detach().cpu() for k in qlinear._keys}
+        # the method's tensors are the module's buffers, named after the method's dict keys
+        self.q = {k: t.detach().cpu() for k, t in qlinear.named_buffers(recurse=False)}
         self.bias = None if qlinear.bias is None else qlinear.bias.detach().cpu().to(dtype)
 
     def forward(self, x):
@@ -74,9 +75,9 @@ class OracleExperts(nn.Module):
         self.name = qexperts.method.name
         self.dtype = dtype
         self.num_experts = qexperts.num_experts
-        keys = qexperts._keys
-        self.gu = {k: getattr(qexperts, f"gate_up_{k}").detach().cpu() for k in keys}
-        self.dn = {k: getattr(qexperts, f"down_{k}").detach().cpu() for k in keys}
+        bufs = dict(qexperts.named_buffers(recurse=False))
+        self.gu = {k[len("gate_up_"):]: t.detach().cpu() for k, t in bufs.items() if k.startswith("gate_up_")}
+        self.dn = {k[len("down_"):]: t.detach().cpu() for k, t in bufs.items() if k.startswith("down_")}
 
     def forward(self, hidden_states, top_k_index, top_k_weights):
         if self.dtype != torch.float32:

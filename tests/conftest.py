@@ -22,3 +22,20 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture
+def miq_env(monkeypatch):
+    """Set MIQ_* kernel-selection variables for one test: libmiq reads them once at load,
+    so the library re-reads them after every change and again after the test."""
+    def reload():
+        from kernels import _lib
+        _lib.load().miq_tuning_reload()
+
+    def setenv(name, value):
+        monkeypatch.setenv(name, value)
+        reload()
+
+    yield setenv
+    monkeypatch.undo()
+    reload()

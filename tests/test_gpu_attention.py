@@ -139,3 +139,50 @@ def test_benchmark_shape(kind):
     got = run(qb, kc, vc, t, sl, 16, 128 ** -0.5, k_scale=ks, v_scale=vs)
     assert rel_error(got, want) < TOL
     within(got, want)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp8", "int8"])
+@pytest.mark.parametrize("partition", [128, 256, 512, 384])
+def test_max_len_below_the_longest_context(kind, partition):
+    """A stale or undersized max_len never cuts a request: when a context does not fit
+    max_parts partitions, its partitions grow (multiples of the partition size) so the
+    whole context is attended, as the reference splits each request's own context
+    (decode_triton.py:25-30, 131-132)."""
+    from kernels.paged_attention import paged_decode_attention
+    case(f"max_len below the context {kind} partition {partition}")
+    lens = [1700, 33, 3000, 1]
+    H, KV, D, page = 16, 4, 128, 16
+    q, k, v, t, sl = random_paged(lens, H, KV, D, page, seed=5)
+    ks = vs = None
+    if kind != "bf16":
+        k, ks = O.kv_quantize(k.float(), kind, torch.float32)
+        v, vs = O.kv_quantize(v.float(), kind, torch.float32)
+    want = A.paged_decode_reference(q, k, v, t, sl, page, D ** -0.5, k_scale=ks, v_scale=vs)
+    for max_len in (partition, 700, 2999):
+        got = paged_decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), t.to(DEV), sl.to(DEV), page, D ** -0.5,
+                                     max_len, k_scale=None if ks is None else ks.to(DEV),
+                                     v_scale=None if vs is None else vs.to(DEV), partition=partition)
+        assert rel_error(got, want) < TOL, max_len
+        within(got, want)
+
+
+@pytest.mark.parametrize("kind", ["bf16", "fp8", "int8"])
+def test_empty_context_rows(kind):
+    """Requests of length 0 (padded batch rows) give zeros and do not disturb the others:
+    the reference's empty split has lse -inf and output 0 (decode_triton.py:95-100)."""
+    case(f"empty contexts {kind}")
+    lens = [0, 300, 0, 17]
+    H, KV, D, page = 8, 2, 128, 16
+    q, k, v, t, sl = random_paged([max(n, 1) for n in lens], H, KV, D, page, seed=6)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    t[0] = 0
+    t[2] = 0
+    ks = vs = None
+    if kind != "bf16":
+        k, ks = O.kv_quantize(k.float(), kind, torch.float32)
+        v, vs = O.kv_quantize(v.float(), kind, torch.float32)
+    got = run(q, k, v, t, sl, page, D ** -0.5, k_scale=ks, v_scale=vs)
+    assert torch.count_nonzero(got[0].float()) == 0 and torch.count_nonzero(got[2].float()) == 0
+    live = torch.tensor([1, 3])
+    want = A.paged_decode_reference(q[live], k, v, t[live], sl[live], page, D ** -0.5, k_scale=ks, v_scale=vs)
+    within(got[live], want)

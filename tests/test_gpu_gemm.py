@@ -84,21 +84,36 @@ INT4_SHAPES = [(1, 64, 256, 128), (5, 128, 512, 128), (8, 64, 1024, 256), (16, 1
                (33, 64, 512, 128), (64, 128, 768, 128), (1, 2560, 9728, 128), (8, 2560, 9728, 128),
                (32, 2560, 9728, 128), (64, 2560, 9728, 128),
                # large groups (a group spans several chunks / the whole split range), ragged N
-               (64, 256, 4096, 1024), (20, 144, 2048, 2048), (1, 512, 8192, 4096), (40, 80, 1024, 256)]
+               (64, 256, 4096, 1024), (20, 144, 2048, 2048), (1, 512, 8192, 4096), (40, 80, 1024, 256),
+               # odd k-step counts and 3-step groups, every activation-tile count, a ragged row block
+               (17, 256, 1152, 384), (48, 1280, 9728, 128), (2, 2560, 9728, 128), (3, 2512, 1152, 128)]
+
+
+PLANS = {"default": {}, "panel": {"MIQ_WO_PANEL": "1"},
+         "panel_s3": {"MIQ_WO_PANEL": "1", "MIQ_WO_PANEL_S": "3"},
+         "panel_s16": {"MIQ_WO_PANEL": "1", "MIQ_WO_PANEL_S": "16"},
+         "panel_mt2": {"MIQ_WO_PANEL": "1", "MIQ_WO_PANEL_MT": "2"},
+         "panel_mt4": {"MIQ_WO_PANEL": "1", "MIQ_WO_PANEL_MT": "4"},
+         "nopanel": {"MIQ_WO_PANEL": "0"},
+         "msplit_4_3": {"MIQ_WO_PANEL": "0"}, "msplit_off": {"MIQ_WO_PANEL": "0"}}
 
 
 @pytest.mark.parametrize("M,N,K,group", INT4_SHAPES)
 @pytest.mark.parametrize("symmetric", [False, True])
-@pytest.mark.parametrize("msplit", [None, "4,3", "0,0"])
-def test_w4a16_gemm(M, N, K, group, symmetric, msplit, monkeypatch):
-    """msplit: the default plan, the M split forced with 4 weight tiles per wavefront and
-    3 splits (one activation tile per workgroup), and the M split turned off."""
+@pytest.mark.parametrize("plan", list(PLANS))
+def test_w4a16_gemm(M, N, K, group, symmetric, plan, miq_env):
+    """plan: the default; the panel kernel forced (split-K panels with a cross-workgroup
+    reduction), with 3 or 16 K splits, or 2 / 4 activation tiles per workgroup; the panel
+    kernel off (the tile / streamed kernels' plan), with the streamed kernel's M split
+    forced to 4 weight tiles per wavefront and 3 splits, or turned off."""
     from kernels import quant_ops as ops
-    if msplit is not None:
+    for k, v in PLANS[plan].items():
+        miq_env(k, v)
+    if plan.startswith("msplit"):
         if M <= 16:
             pytest.skip("the M split applies to more than 16 rows")
-        monkeypatch.setenv("MIQ_WO_MSPLIT", msplit)
-    case(f"w4a16 M={M} N={N} K={K} g={group} sym={symmetric} msplit={msplit}")
+        miq_env("MIQ_WO_MSPLIT", "4,3" if plan == "msplit_4_3" else "0,0")
+    case(f"w4a16 M={M} N={N} K={K} g={group} sym={symmetric} plan={plan}")
     w = make_w(N, K, 20)
     x = make_x(M, K, 21)
     q = O.int4_quantize_symmetric(w, group) if symmetric else O.int4_quantize(w, group)
@@ -133,20 +148,21 @@ def test_w4a16_scale_dtypes(sdt):
 TILE_CASES = [(1, 320, 9728, 128), (4, 320, 9728, 128), (3, 160, 1152, 128), (2, 96, 1152, 384),
               (8, 64, 4096, 512), (16, 64, 1024, 128), (7, 48, 2560, 256), (1, 2560, 9728, 128),
               (5, 3008, 2048, 128)]
-# kernel choice: the default plan, the streamed kernel, and the tile kernel with a forced
-# number of weight rows per tile (16, and 7: a tile whose 128-byte loads are partly empty)
-KERNELS = {"auto": {}, "stream": {"MIQ_WO_STREAM": "1"}, "rows16": {"MIQ_WO_ROWS": "16"},
-           "rows7": {"MIQ_WO_ROWS": "7"}}
+# kernel choice: the default plan (INT4: the panel kernel), the plan without the panel
+# kernel, the streamed kernel, and the tile kernel with a forced number of weight rows per
+# tile (16, and 7: a tile whose 128-byte loads are partly empty)
+KERNELS = {"auto": {}, "nopanel": {"MIQ_WO_PANEL": "0"}, "stream": {"MIQ_WO_STREAM": "1"},
+           "rows16": {"MIQ_WO_ROWS": "16", "MIQ_WO_PANEL": "0"}, "rows7": {"MIQ_WO_ROWS": "7", "MIQ_WO_PANEL": "0"}}
 
 
 @pytest.mark.parametrize("kernel", list(KERNELS))
 @pytest.mark.parametrize("M,N,K,group", TILE_CASES)
 @pytest.mark.parametrize("sdt,symmetric", [(torch.bfloat16, True), (torch.float32, False), (torch.float16, False)])
-def test_w4a16_tile_and_stream(kernel, M, N, K, group, sdt, symmetric, monkeypatch):
+def test_w4a16_tile_and_stream(kernel, M, N, K, group, sdt, symmetric, miq_env):
     from kernels import quant_ops as ops
     case(f"w4a16 {kernel} M={M} N={N} K={K} g={group} {sdt} sym={symmetric}")
     for k, v in KERNELS[kernel].items():
-        monkeypatch.setenv(k, v)
+        miq_env(k, v)
     w = make_w(N, K, 50)
     x = make_x(M, K, 51)
     q = O.int4_quantize_symmetric(w, group) if symmetric else O.int4_quantize(w, group)
@@ -161,11 +177,11 @@ def test_w4a16_tile_and_stream(kernel, M, N, K, group, sdt, symmetric, monkeypat
 
 @pytest.mark.parametrize("kernel", list(KERNELS))
 @pytest.mark.parametrize("M,N,K", [(1, 19456, 2560), (2, 4096, 2560), (3, 160, 1152), (4, 64, 9728), (1, 2512, 2560)])
-def test_w8a16_tile_and_stream(kernel, M, N, K, monkeypatch):
+def test_w8a16_tile_and_stream(kernel, M, N, K, miq_env):
     from kernels import quant_ops as ops
     case(f"w8a16 {kernel} M={M} N={N} K={K}")
     for k, v in KERNELS[kernel].items():
-        monkeypatch.setenv(k, v)
+        miq_env(k, v)
     w = make_w(N, K, 52)
     x = make_x(M, K, 53)
     q = O.int8_quantize(w, torch.float32)
@@ -182,10 +198,10 @@ def test_split_k_repeated_calls_are_identical():
     q = O.int4_quantize(w, 128)
     qd = {k: v.to(DEV) for k, v in q.items()}
     outs = []
-    for M in (1, 8, 1, 8):
+    for M in (1, 8, 64, 1, 8, 64, 33, 33):
         x = make_x(M, 9728, 31).to(DEV)
         outs.append(ops.w4a16_linear(x, qd["qweight"], qd["scale"], qd["zero"]).cpu())
-    assert torch.equal(outs[0], outs[2]) and torch.equal(outs[1], outs[3])
+    assert all(torch.equal(outs[i], outs[i + 3]) for i in range(3)) and torch.equal(outs[6], outs[7])
 
 
 @pytest.mark.parametrize("name", ["int8_wo", "int4_wo", "fp8"])
@@ -234,3 +250,35 @@ def test_fp8_linear_end_to_end():
     within(y, O.fp8_scaled_mm(xq, xs, **wq))
     emu = O.fp8_linear_emulated(x, **wq)
     assert ((y.float().cpu() - emu.float()).norm() / emu.float().norm()).item() < 0.02
+
+
+@pytest.mark.parametrize("M", [1, 8, 32, 64])
+@pytest.mark.parametrize("symmetric", [True, False])
+def test_w4a16_elementwise_vs_reference_formula(M, symmetric):
+    """Config 2 (N = 2560, K = 9728, group 128): the fused kernel against the reference's
+    own formula, dequantize to bf16 then F.linear (int4_wo.py:33-42, base.py:20-24),
+    element by element. The kernel multiplies the exactly dequantized weights (q * s + z
+    in fp32); the reference rounds each one to bf16 (twice with zero points). The two
+    results therefore differ by at most |x| @ |w_ref - w_exact|^T (the weight rounding,
+    computed here exactly) plus one bf16 rounding of each output and fp32 accumulation
+    noise; every element must lie within that bound."""
+    from kernels import quant_ops as ops
+    case(f"w4a16 vs reference formula M={M} sym={symmetric}")
+    N, K = 2560, 9728
+    w = make_w(N, K, 60)
+    x = make_x(M, K, 61)
+    q = O.int4_quantize_symmetric(w, 128) if symmetric else O.int4_quantize(w, 128)
+    got = ops.w4a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV),
+                           None if symmetric else q["zero"].to(DEV)).float().cpu()
+    ref = O.int4_linear(x, **q).float()                          # the reference's bf16 formula
+    w_ref = O.int4_dequantize(**q).double()
+    qs = O.int4_unpack(q["qweight"]).double().reshape(N, K // 128, 128)
+    s = q["scale"].double().unsqueeze(-1)
+    w_exact = ((qs - 8) * s if symmetric else qs * s + q["zero"].double().unsqueeze(-1)).reshape(N, K)
+    xd = x.double()
+    explained = xd.abs() @ (w_ref - w_exact).abs().t()
+    bound = explained + 2.0 ** -8 * (got.abs() + ref.abs()).double() + 1e-3
+    diff = (got.double() - ref.double()).abs()
+    print(f"[bound] M={M} sym={symmetric}: max |kernel - reference| {diff.max().item():.4f}, "
+          f"max of diff / bound {(diff / bound).max().item():.3f}", flush=True)
+    assert (diff <= bound).all()

@@ -21,7 +21,7 @@ def rel_error(a, b):
                                        (4096, 8, 64, 64), (64, 8, 64, 16)])
 @pytest.mark.parametrize("dtype", [torch.int64, torch.int32])
 @pytest.mark.parametrize("path", ["auto", "scan"])
-def test_moe_align_matches_oracle_exactly(T, k, E, bm, dtype, path, monkeypatch):
+def test_moe_align_matches_oracle_exactly(T, k, E, bm, dtype, path, miq_env):
     """The HIP kernel places pairs in ascending order inside each expert, so its output
     equals the oracle's stable restatement element for element (a stronger check than the
     grouping equality of reference tests/test_fused_moe.py:56-88). "auto" takes the
@@ -29,7 +29,7 @@ def test_moe_align_matches_oracle_exactly(T, k, E, bm, dtype, path, monkeypatch)
     one-wavefront-per-expert kernel."""
     from kernels.fused_moe import moe_align
     if path == "scan":
-        monkeypatch.setenv("MIQ_MOE_ALIGN_SCAN", "1")
+        miq_env("MIQ_MOE_ALIGN_SCAN", "1")
     case(f"moe_align T={T} k={k} E={E} bm={bm} {dtype} {path}")
     g = torch.Generator().manual_seed(T)
     ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(dtype)
@@ -104,3 +104,35 @@ def test_quant_experts_module_uses_fused_path():
     dn = {kk: getattr(qe, f"down_{kk}").cpu() for kk in ("qweight", "scale", "zero")}
     want = MO.int4_experts_reference(hidden, gu, dn, w, idx)
     assert rel_error(fused, want) < 2e-2
+
+
+@pytest.mark.parametrize("sym", [False, True])
+def test_fused_moe_fp32_routing_weights_vs_reference_loop(sym):
+    """Routing weights in fp32 (a router that keeps fp32 probabilities): the fused layer uses
+    them in their own dtype, as the reference loop multiplies by them (modules.py:55-75),
+    and adds each token's expert contributions in ascending expert order with a bf16
+    rounding after each addition (index_add_ into a bf16 output). Against the reference
+    loop with the reference's own INT4 formula (dequantize to bf16, then F.linear), every
+    element lies within the loop's own distance to the exact fp32 experts plus the
+    north-star tolerance; the distance of each to the exact reference is printed."""
+    from kernels.fused_moe import fused_moe_int4
+    case(f"fused int4 moe fp32 weights sym={sym}")
+    T, H, I, E, k = 64, 2048, 1024, 64, 8
+    g = torch.Generator().manual_seed(11)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
+    wdn = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)
+    qf = O.int4_quantize_symmetric if sym else O.int4_quantize
+    gu, dn = qf(wgu, 128), qf(wdn, 128)
+    hidden, _, idx = routed(T, H, E, k, seed=12)
+    router = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16)
+    w32 = torch.softmax(hidden.float() @ router.float().t(), dim=-1).gather(1, idx)  # fp32 weights
+    loop = MO.quant_experts_loop(hidden, O.int4_linear, gu, dn, idx, w32, E).float()
+    exact = MO.int4_experts_reference(hidden, gu, dn, w32, idx)
+    got = fused_moe_int4(hidden.to(DEV), idx.to(DEV), w32.to(DEV), gu["qweight"].to(DEV), gu["scale"].to(DEV),
+                         None if sym else gu["zero"].to(DEV), dn["qweight"].to(DEV), dn["scale"].to(DEV),
+                         None if sym else dn["zero"].to(DEV)).float().cpu()
+    d_got, d_loop = (got - exact).abs(), (loop - exact).abs()
+    print(f"[bound] moe sym={sym}: max |fused - exact| {d_got.max().item():.4f}, max |loop - exact| "
+          f"{d_loop.max().item():.4f}, max |fused - loop| {(got - loop).abs().max().item():.4f}", flush=True)
+    assert ((got - loop).abs() <= d_loop + 1e-2 + 2e-2 * loop.abs()).all()
+    assert rel_error(got, exact) < 2e-2
