@@ -119,6 +119,18 @@ int miq_w4a16_gemm(const void* x, int64_t ldx, const uint8_t* q, const void* sca
                    int64_t M, int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
                    void* stream);
 
+/* miq_w4a16_gemm without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. The split-K scratch is a static device array
+ * of 32 MiB that each GPU holds until the process ends; shapes whose
+ * miq_wo_gemm_workspace_bytes(M, N, K, 4) exceeds it are rejected (MIQ_ERR_INVALID). Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams, two threads) race and give wrong results; calls ordered
+ * on one stream are safe. Allocates nothing; the first call on a device looks up the
+ * array's address there. Same arguments and results as miq_w4a16_gemm. */
+int miq_w4a16_gemm_noalloc(const void* x, int64_t ldx, const uint8_t* q, const void* scale,
+                           const void* zero, int sz_dtype, int64_t group, void* y, int64_t ldy,
+                           int64_t M, int64_t N, int64_t K, void* stream);
+
 /* ------------------------------------------------------------------ FP8 prefill GEMM
  * Replaces the torch._scaled_mm call of FP8WeightAct.linear (fp8.py:55-61):
  *   y[m, n] = bf16( (sum_k xq[m,k] * wq[n,k]) * x_scale[m] * w_scale[n] )

@@ -5,6 +5,7 @@
 // Argument checks live here. Up to 16 rows whose activations fit LDS run the one-tile-per-
 // workgroup kernel (wo_tile.hip); the rest the streamed split-K kernel (wo_stream.hip).
 #include <algorithm>
+#include <mutex>
 
 #include "wo_core.h"
 
@@ -126,4 +127,51 @@ extern "C" int miq_w4a16_gemm(const void* x, int64_t ldx, const uint8_t* q, cons
   p.N = (int)N;
   p.K = (int)K;
   return run(KIND_INT4, p, workspace, workspace_bytes, (hipStream_t)stream, "w4a16_gemm");
+}
+
+// ------------------------------------------------------------------ no-allocation variant
+// miq_w4a16_gemm_noalloc takes the split-K scratch (counters and partials) from a
+// file-scope device array instead of a caller's workspace. Each GPU holds its own copy of
+// the array (zero at load; every call leaves it zero again) until the process ends. Its
+// address is looked up once per device, with that device current, on the first call there;
+// host code uses only that address, never the array's name.
+namespace {
+constexpr size_t kScratchBytes = (size_t)32 << 20;  // per GPU
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+std::mutex g_scratch_lock;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  MIQ_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices,
+              "w4a16_gemm_noalloc: no current device (or device id above %d)", kMaxDevices - 1);
+  std::lock_guard<std::mutex> hold(g_scratch_lock);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("w4a16_gemm_noalloc: hipGetSymbolAddress of the scratch array failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return MIQ_ERR_LAUNCH;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MIQ_OK;
+}
+}  // namespace
+
+extern "C" int miq_w4a16_gemm_noalloc(const void* x, int64_t ldx, const uint8_t* q, const void* scale,
+                                      const void* zero, int sz_dtype, int64_t group, void* y, int64_t ldy,
+                                      int64_t M, int64_t N, int64_t K, void* stream) {
+  const size_t need = miq_wo_gemm_workspace_bytes(M, N, K, 4);
+  MIQ_REQUIRE(need <= kScratchBytes,
+              "w4a16_gemm_noalloc: M=%lld N=%lld K=%lld needs %zu bytes of split-K scratch, above the %zu bytes "
+              "the library holds per GPU; use miq_w4a16_gemm with a workspace",
+              (long long)M, (long long)N, (long long)K, need, kScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_of_current_device(&ws);
+  if (rc != MIQ_OK) return rc;
+  return miq_w4a16_gemm(x, ldx, q, scale, zero, sz_dtype, group, y, ldy, M, N, K, ws, kScratchBytes, stream);
 }

@@ -44,6 +44,7 @@ SIGNATURES = {
     "miq_wo_gemm_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I32]),
     "miq_w8a16_gemm": (_I32, [_P, _I64, _P, _P, _I32, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P]),
     "miq_w4a16_gemm": (_I32, [_P, _I64, _P, _P, _P, _I32, _I64, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P]),
+    "miq_w4a16_gemm_noalloc": (_I32, [_P, _I64, _P, _P, _P, _I32, _I64, _P, _I64, _I64, _I64, _I64, _P]),
     "miq_fp8_gemm": (_I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _P]),
     "miq_kv_quant_write": (_I32, [_P, _I32, _I64, _I64, _I64, _I64, _I64, _P, _P, _I32, _I64, _I64,
                                   _P, _I32, _I64, _I64, _P]),

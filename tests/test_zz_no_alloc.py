@@ -1,0 +1,71 @@
+"""miq_w4a16_gemm_noalloc (the entry point that allocates nothing: its split-K scratch is a
+static device array) against miq_w4a16_gemm with a caller workspace, through the C ABI.
+Both run the same kernels with the same plans, so the outputs must be identical bytes;
+two calls in a row, the second smaller, then the first again (the scratch is left clean)."""
+import ctypes
+
+import pytest
+import torch
+
+from oracle import quant as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def operands(M, N, K, group, symmetric, seed):
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    q = O.int4_quantize_symmetric(w, group) if symmetric else O.int4_quantize(w, group)
+    return x.to(DEV), {k: v.to(DEV) for k, v in q.items()}
+
+
+def noalloc(x, q, group):
+    from kernels import _lib as L
+    M, K = x.shape
+    N = q["qweight"].shape[0]
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=DEV)
+    z = q.get("zero")
+    rc = L.load().miq_w4a16_gemm_noalloc(
+        L.ptr(x), x.stride(0), L.ptr(q["qweight"]), L.ptr(q["scale"]), L.ptr(z), L.dtype_code(q["scale"].dtype),
+        group, L.ptr(y), y.stride(0), M, N, K, L.stream(x.device))
+    return rc, y
+
+
+def with_workspace(x, q):
+    from kernels import quant_ops as ops
+    return ops.w4a16_linear(x, q["qweight"], q["scale"], q.get("zero"))
+
+
+def test_noalloc_matches_workspace_entry_point():
+    # (M, N, K, group, symmetric): the panel kernel with its largest scratch at config 2, a
+    # smaller panel launch, a tile-kernel launch (no scratch), then the first shape again
+    shapes = [(64, 2560, 9728, 128, True), (40, 1280, 4096, 256, False), (8, 512, 1024, 128, False),
+              (64, 2560, 9728, 128, True)]
+    for i, (M, N, K, group, sym) in enumerate(shapes):
+        case(f"noalloc call {i}: M={M} N={N} K={K} g={group} sym={sym}")
+        x, q = operands(M, N, K, group, sym, seed=70 + (i % 3))
+        rc, y = noalloc(x, q, group)
+        assert rc == 0
+        want = with_workspace(x, q)
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), (y.float() - want.float()).abs().max().item()
+        # and within the north-star tolerance of the fp32 oracle
+        ref = O.int4_linear_fp32(x.cpu(), **{k: v.cpu() for k, v in q.items()})
+        err = (y.float().cpu() - ref).abs()
+        assert (err <= 1e-2 + 2e-2 * ref.abs()).all()
+
+
+def test_noalloc_rejects_shapes_beyond_the_scratch():
+    from kernels import _lib as L
+    case("noalloc rejects a shape beyond its scratch")
+    M, N, K = 64, 16384 * 8, 9728  # split-K partials well above 32 MiB
+    assert L.load().miq_wo_gemm_workspace_bytes(M, N, K, 4) > 32 << 20
+    rc = L.load().miq_w4a16_gemm_noalloc(None, K, None, None, None, L.MIQ_BF16, 128, None, N, M, N, K, None)
+    assert rc == -1
+    assert b"above the" in L.load().miq_last_error()
