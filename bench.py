@@ -10,17 +10,31 @@ The timed region is one replay of a HIP graph holding exactly --steps steps, bra
 torch.cuda.synchronize() and HIP events on the stream the kernels run on; the average
 kernel duration is that time / (4 * steps) (the launches run back to back in the graph).
 
-`breakdown` reports the other configurations the same way (INT8 gate_up GEMM, FP8
-prefill GEMM, paged decode attention on FP8 / INT8 KV, INT4 MoE layer); `cpu_baseline`
-times the reference formulas restated on the CPU (oracle/) on a bounded sample.
+`roofline.traffic` (HBM bytes per headline launch) comes from two rocprofv3 counter passes
+(FETCH_SIZE, then WRITE_SIZE) over a short child run of the same four launches, made before
+this process touches the GPU; each counter is scaled by its reading for a reference kernel
+of known size in the same child run (a 256 MiB sum for FETCH_SIZE, a 256 MiB fill for
+WRITE_SIZE). Without rocprofv3 it is null.
 
-Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--only headline]
+`breakdown` reports the other configurations the same way (INT8 gate_up GEMM, FP8 prefill
+GEMM, paged decode attention on FP8 / INT8 KV at the 256-token default and the configuration's
+512-token partition with two KV copies alternating, INT4 MoE layer), each with a CPU number:
+`cpu_baseline` times the reference formulas restated on the CPU (oracle/) on a bounded
+sample of the same configuration.
+
+Usage: python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--no-cpu] [--no-traffic]
+                       [--only headline]
 """
 import argparse
+import csv
+import glob
 import json
 import math
 import os
+import shutil
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -35,11 +49,7 @@ FP8_PEAK_TFLOPS = 5000.0     # MI355X dense FP8 MFMA, published
 ROTATE_BYTES = 600 * 2 ** 20  # > 2 x MALL
 METRIC = "quantized decode GEMM GB/s (% HBM peak) at M=1..64; FP8-KV attn µs/step"
 MS = (1, 8, 32, 64)
-# HBM bytes per headline launch (mean over M = 1, 8, 32, 64), from rocprofv3 FETCH_SIZE /
-# WRITE_SIZE passes of `bench.py --only headline --copy-probe`, scaled by the counters'
-# readings for a 256 MiB sum and fill (profiles/wo_int4_headline_traffic.md).
-# Re-measure when the kernel changes.
-HEADLINE_TRAFFIC_BYTES = 21_413_092
+PROBE_BYTES = 256 * 2 ** 20   # size of the counter-calibration sum / fill
 
 
 def log(*a):
@@ -74,6 +84,16 @@ def time_graph(fn_list, reps=1):
     end.record(stream)
     torch.cuda.synchronize()
     return start.elapsed_time(end) / 1e3 / reps
+
+
+def host_cpu():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
 
 
 # ---------------------------------------------------------------- configurations
@@ -175,7 +195,8 @@ def bench_fp8(dev):
             "quant+gemm_TFLOP/s": round(tf_all, 1), "peak_used_TFLOP/s": FP8_PEAK_TFLOPS}
 
 
-def attention_inputs(dev, kind, B=64, H=32, KV=8, D=128, page=16, seed=7):
+def attention_tables(B=64, page=16, seed=7):
+    """Context lengths U[512, 8192] and a shuffled block table over all pages (seeded)."""
     g = gen(seed)
     lens = torch.randint(512, 8193, (B,), generator=g)
     pages = [-(-int(n) // page) for n in lens]
@@ -186,33 +207,42 @@ def attention_inputs(dev, kind, B=64, H=32, KV=8, D=128, page=16, seed=7):
     for b, n in enumerate(pages):
         table[b, :n] = perm[i:i + n].to(torch.int32)
         i += n
-    slots = total * page
-    # K/V ~ N(0,1) generated on the device from a seeded generator (570 MB of codes)
-    dg = torch.Generator(device=dev).manual_seed(seed)
-    k = torch.randn(slots, KV, D, generator=dg, device=dev)
-    v = torch.randn(slots, KV, D, generator=dg, device=dev)
-    if kind == "fp8":
-        s = torch.tensor(4.0 / 448.0, device=dev)
-        kc = (k / s).clamp(-448, 448).to(torch.float8_e4m3fn)
-        vc = (v / s).clamp(-448, 448).to(torch.float8_e4m3fn)
-        ks = s.reshape(1, 1).expand(slots, KV)
-        vs = ks
-        scale_bytes = 0
-    else:
-        from engine.core.kv_cache import kv_quant_write
-        kc = torch.empty(slots, KV, D, dtype=torch.int8, device=dev)
-        vc = torch.empty_like(kc)
-        ks = torch.empty(slots, KV, dtype=torch.float32, device=dev)
-        vs = torch.empty_like(ks)
-        idx = torch.arange(slots, device=dev)
-        kv_quant_write(kc, ks, idx, k)
-        kv_quant_write(vc, vs, idx, v)
-        scale_bytes = int(lens.sum()) * KV * 2 * 4
-    del k, v
+    return g, lens, pages, table
+
+
+def attention_inputs(dev, kind, B=64, H=32, KV=8, D=128, page=16, seed=7, copies=2):
+    """Config 4: `copies` independent KV caches (> 2 x the MALL together) so consecutive
+    calls never read a cache the previous call left in the MALL."""
+    g, lens, pages, table = attention_tables(B, page, seed)
+    slots = sum(pages) * page
+    caches = []
+    for c in range(copies):
+        # K/V ~ N(0,1) generated on the device from a seeded generator (570 MB of codes)
+        dg = torch.Generator(device=dev).manual_seed(seed + 100 * c)
+        k = torch.randn(slots, KV, D, generator=dg, device=dev)
+        v = torch.randn(slots, KV, D, generator=dg, device=dev)
+        if kind == "fp8":
+            s = torch.tensor(4.0 / 448.0, device=dev)
+            kc = (k / s).clamp(-448, 448).to(torch.float8_e4m3fn)
+            vc = (v / s).clamp(-448, 448).to(torch.float8_e4m3fn)
+            ks = s.reshape(1, 1).expand(slots, KV)
+            vs = ks
+        else:
+            from engine.core.kv_cache import kv_quant_write
+            kc = torch.empty(slots, KV, D, dtype=torch.int8, device=dev)
+            vc = torch.empty_like(kc)
+            ks = torch.empty(slots, KV, dtype=torch.float32, device=dev)
+            vs = torch.empty_like(ks)
+            idx = torch.arange(slots, device=dev)
+            kv_quant_write(kc, ks, idx, k)
+            kv_quant_write(vc, vs, idx, v)
+        del k, v
+        caches.append((kc, vc, ks, vs))
+    scale_bytes = 0 if kind == "fp8" else int(lens.sum()) * KV * 2 * 4
     q = torch.randn(B, H, D, generator=g).to(torch.bfloat16).to(dev)
     ntok = int(lens.sum())
     nbytes = ntok * KV * D * 2 + scale_bytes + sum(pages) * 4 + B * H * D * 2 * 2 + B * 4
-    return dict(q=q, k=kc, v=vc, ks=ks, vs=vs, table=table.to(dev), lens=lens.to(torch.int32).to(dev),
+    return dict(q=q, caches=caches, table=table.to(dev), lens=lens.to(torch.int32).to(dev),
                 max_len=int(lens.max()), page=page, bytes=nbytes, tokens=ntok)
 
 
@@ -220,27 +250,37 @@ def bench_attention(dev, kind):
     from kernels.paged_attention import paged_decode_attention
     a = attention_inputs(dev, kind)
 
-    def f():
-        return paged_decode_attention(a["q"], a["k"], a["v"], a["table"], a["lens"], a["page"], 128 ** -0.5,
-                                      8192, k_scale=a["ks"], v_scale=a["vs"])
+    def call(i, partition):
+        kc, vc, ks, vs = a["caches"][i % len(a["caches"])]
+        return lambda: paged_decode_attention(a["q"], kc, vc, a["table"], a["lens"], a["page"], 128 ** -0.5,
+                                              a["max_len"], k_scale=ks, v_scale=vs, partition=partition)
     reps = 20
-    t = time_graph([f] * reps) / reps
-    gbs = a["bytes"] / t / 1e9
-    res = {"us_per_step": round(t * 1e6, 2), "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
-           "context_tokens": a["tokens"], "MB_per_call": round(a["bytes"] / 1e6, 1)}
+    res = {"context_tokens": a["tokens"], "MB_per_call": round(a["bytes"] / 1e6, 1), "kv_copies": len(a["caches"])}
+    for partition in (256, 512):
+        t = time_graph([call(i, partition) for i in range(reps)]) / reps
+        gbs = a["bytes"] / t / 1e9
+        res[f"partition_{partition}"] = {"us_per_step": round(t * 1e6, 2), "GB/s": round(gbs, 1),
+                                         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1)}
+    res["default_partition"] = 256
     del a
     return res
+
+
+def moe_routing(T=64, H=2048, E=64, k=8, seed=8):
+    """bench/micro/bench_moe.py:113-117: softmax over a bf16 router, top-k, no renorm."""
+    g = gen(seed)
+    hidden = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    router = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16)
+    probs = torch.softmax(hidden.float() @ router.float().t(), dim=-1)
+    w, idx = torch.topk(probs, k, dim=-1)
+    return hidden, w.to(torch.bfloat16), idx
 
 
 def moe_setup(dev, copies=None):
     from kernels import quant_ops as ops
     T, H, inter, E, k = 64, 2048, 1024, 64, 8
-    g = gen(8)
-    hidden = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
-    router = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16).to(dev)
-    probs = torch.softmax(hidden.float() @ router.float().t(), dim=-1)
-    w, idx = torch.topk(probs, k, dim=-1)
-    w = w.to(torch.bfloat16)
+    hidden, w, idx = moe_routing(T, H, E, k)
+    hidden, w, idx = hidden.to(dev), w.to(dev), idx.to(dev)
     dg = torch.Generator(device=dev).manual_seed(9)
     wgu = (torch.randn(E, 2 * inter, H, generator=dg, device=dev) * 0.02).to(torch.bfloat16)
     wdn = (torch.randn(E, H, inter, generator=dg, device=dev) * 0.02).to(torch.bfloat16)
@@ -272,43 +312,190 @@ def bench_moe(dev):
     return res
 
 
-# ---------------------------------------------------------------- CPU baseline (oracle)
-def cpu_baseline_headline(budget_s=20.0):
-    """The reference's CPU path for the headline step: Int4WeightOnly.linear =
-    dequantize (int4_wo.py:33-42) + F.linear (base.py:20-24), restated in oracle/quant.py,
-    at the four M values; bounded: as many whole steps as fit in ~budget_s (at least one)."""
+# ---------------------------------------------------------------- CPU baselines (oracle)
+# The reference's CPU path restated in oracle/ (plain PyTorch), on the host cores of the
+# GPU box, at each configuration's shape; a bounded sample: whole calls until about
+# `budget` seconds have passed (at least one), median time. Same units as the GPU lines.
+def _cpu_time(fn, budget):
+    fn()  # warm-up
+    times, t_start = [], time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget or len(times) >= 10:
+            break
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def _cpu_line(value, unit, n, what):
+    return {"value": value, "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{n} {what}; median; oracle/ restatement of the reference's CPU path; {host_cpu()}; "
+                      f"torch {torch.__version__}"}
+
+
+def cpu_int4_headline(budget=6.0):
+    """Int4WeightOnly.linear = dequantize (int4_wo.py:33-42) + F.linear (base.py:20-24)."""
     from oracle import quant as O
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
     N, K = 2560, 9728
     w = (torch.randn(N, K, generator=gen(2)) * 0.02).to(torch.bfloat16)
     q = O.int4_quantize_symmetric(w, 128)
     xs = {M: torch.randn(M, K, generator=gen(3)).to(torch.bfloat16) for M in MS}
-    O.int4_linear(xs[1], **q)  # warm-up
     wbytes = q["qweight"].numel() + q["scale"].numel() * 2
     step_bytes = sum(wbytes + M * K * 2 + M * N * 2 for M in MS)
-    times = []
-    t_start = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        for M in MS:
-            O.int4_linear(xs[M], **q)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 10:
-            break
-    times.sort()
-    t = times[len(times) // 2]
-    cpu = "unknown"
+    t, n = _cpu_time(lambda: [O.int4_linear(xs[M], **q) for M in MS], budget)
+    return _cpu_line(round(step_bytes / t / 1e9, 3), "GB/s", n,
+                     f"whole steps (4 INT4 linears, M=1/8/32/64, N=2560 K=9728), {t * 1e3:.1f} ms/step")
+
+
+def cpu_int8(budget=6.0):
+    """Int8WeightOnly.linear (int8_wo.py:17-21) at the gate_up shape, M=1/8/32/64."""
+    from oracle import quant as O
+    N, K = 19456, 2560
+    w = (torch.randn(N, K, generator=gen(1)) * 0.02).to(torch.bfloat16)
+    q = O.int8_quantize(w, torch.float32)
+    xs = {M: torch.randn(M, K, generator=gen(4)).to(torch.bfloat16) for M in MS}
+    step_bytes = sum(N * K + N * 4 + M * K * 2 + M * N * 2 for M in MS)
+    t, n = _cpu_time(lambda: [O.int8_linear(xs[M], **q) for M in MS], budget)
+    return _cpu_line(round(step_bytes / t / 1e9, 3), "GB/s", n,
+                     f"steps of 4 INT8 linears (M=1/8/32/64, N=19456 K=2560), {t * 1e3:.1f} ms/step")
+
+
+def cpu_fp8(budget=6.0):
+    """FP8WeightAct.linear on the CPU: activation quantize + the emulated matmul
+    (fp8.py:41-46, 69-73), what the reference runs without native FP8."""
+    from oracle import quant as O
+    M, N, K = 2048, 6144, 2560
+    w = (torch.randn(N, K, generator=gen(5)) * 0.02).to(torch.bfloat16)
+    q = O.fp8_quantize(w)
+    x = torch.randn(M, K, generator=gen(6)).to(torch.bfloat16)
+    t, n = _cpu_time(lambda: O.fp8_linear_emulated(x, **q), budget)
+    return _cpu_line(round(2.0 * M * N * K / t / 1e12, 4), "TFLOP/s", n,
+                     f"calls at 2048x6144x2560 (activation quant + emulated GEMM), {t * 1e3:.1f} ms/call")
+
+
+def cpu_attention(kind, budget=6.0, requests=16):
+    """The per-request fp32 loop of paged_attention/reference.py:10-28 over the config-4
+    cache; sample: the first `requests` requests of the batch."""
+    from oracle import attention as A
+    from oracle import quant as O
+    KV, D, H, page = 8, 128, 32, 16
+    g, lens, pages, table = attention_tables(64, page, 7)
+    lens, table = lens[:requests], table[:requests]
+    slots = (int(table.max()) + 1) * page
+    kg = torch.Generator().manual_seed(107)
+    k = torch.randn(slots, KV, D, generator=kg)
+    v = torch.randn(slots, KV, D, generator=kg)
+    if kind == "fp8":
+        s = torch.tensor(4.0 / 448.0)
+        kc = (k / s).clamp(-448, 448).to(torch.float8_e4m3fn)
+        vc = (v / s).clamp(-448, 448).to(torch.float8_e4m3fn)
+        ks = s.reshape(1, 1).expand(slots, KV)
+        vs = ks
+    else:
+        kc, ks = O.kv_quantize(k, "int8", torch.float32)
+        vc, vs = O.kv_quantize(v, "int8", torch.float32)
+    del k, v
+    q = torch.randn(requests, H, D, generator=g).to(torch.bfloat16)
+    ntok = int(lens.sum())
+    nbytes = ntok * KV * D * 2 + (0 if kind == "fp8" else ntok * KV * 2 * 4) + ntok // page * 4 + requests * H * D * 4
+    t, n = _cpu_time(lambda: A.paged_decode_reference(q, kc, vc, table, lens, page, D ** -0.5, k_scale=ks,
+                                                      v_scale=vs), budget)
+    return _cpu_line(round(nbytes / t / 1e9, 3), "GB/s", n,
+                     f"calls over {requests} of the 64 requests ({ntok} context tokens), {t * 1e3:.1f} ms/call")
+
+
+def cpu_moe(budget=6.0):
+    """QuantExperts.forward's per-expert loop (modules.py:55-75) with the INT4 method's
+    dequantize + F.linear, at config 5."""
+    from oracle import moe as MO
+    from oracle import quant as O
+    T, H, inter, E, k = 64, 2048, 1024, 64, 8
+    hidden, w, idx = moe_routing(T, H, E, k)
+    g = gen(9)
+    gu = O.int4_quantize_symmetric((torch.randn(E, 2 * inter, H, generator=g) * 0.02).to(torch.bfloat16), 128)
+    dn = O.int4_quantize_symmetric((torch.randn(E, H, inter, generator=g) * 0.02).to(torch.bfloat16), 128)
+    touched = int(idx.unique().numel())
+    per_expert = (2 * inter * H // 2 + H * inter // 2) + (2 * inter * H // 128 + H * inter // 128) * 2
+    nbytes = touched * per_expert + T * H * 2 * 2 + T * k * 6
+    t, n = _cpu_time(lambda: MO.quant_experts_loop(hidden, O.int4_linear, gu, dn, idx, w, E), budget)
+    return _cpu_line(round(nbytes / t / 1e9, 3), "GB/s", n, f"layer calls (64 tokens, top-8 of 64 experts), "
+                     f"{t * 1e3:.1f} ms/call")
+
+
+# ---------------------------------------------------------------- HBM traffic (counters)
+def traffic_child():
+    """The run the counter passes watch: four headline launches per round, eagerly, then
+    the two calibration kernels (a 256 MiB fill, and a sum over a 256 MiB buffer that a
+    second fill has evicted from the MALL)."""
+    from kernels import _lib
+    _lib.load()
+    dev = torch.device("cuda:0")
+    cfg = int4_setup(dev)
+    for i in range(3):
+        for j, M in enumerate(MS):
+            int4_launch(cfg, M, 4 * i + j)()
+    torch.cuda.synchronize()
+    del cfg
+    torch.cuda.empty_cache()
+    a = torch.empty(PROBE_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    b = torch.empty_like(a).fill_(2.0)
+    a.sum()
+    torch.cuda.synchronize()
+    del a, b
+
+
+def _pmc_pass(counter, outdir):
+    cmd = ["rocprofv3", "--pmc", counter, "--output-format", "csv", "-d", outdir, "-o", "run", "--",
+           sys.executable, os.path.abspath(__file__), "--traffic-child"]
+    env = dict(os.environ, TMPDIR="/tmp")
+    subprocess.run(["timeout", "-s", "KILL", "150"] + cmd, cwd="/tmp", env=env, check=True,
+                   stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
+    rows = []
+    for path in glob.glob(os.path.join(outdir, "**", "*counter_collection.csv"), recursive=True):
+        with open(path, newline="") as f:
+            rows += [r for r in csv.DictReader(f) if r["Counter_Name"] == counter]
+    rows.sort(key=lambda r: int(r["Dispatch_Id"]))
+    return rows
+
+
+def measure_traffic():
+    """Per-launch HBM bytes of the headline kernels from FETCH_SIZE and WRITE_SIZE passes.
+    Returns (dict, None) or (None, reason)."""
+    if shutil.which("rocprofv3") is None:
+        return None, "rocprofv3 not found"
+    tmp = tempfile.mkdtemp(prefix="miq_traffic_", dir="/tmp")
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": round(step_bytes / t / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"{len(times)} whole steps (4 INT4 linears, M=1/8/32/64, N=2560 K=9728), median "
-                      f"{t * 1e3:.1f} ms/step; oracle int4 dequantize + F.linear in bf16; {cpu}; torch {torch.__version__}"}
+        fetch = _pmc_pass("FETCH_SIZE", os.path.join(tmp, "fetch"))
+        write = _pmc_pass("WRITE_SIZE", os.path.join(tmp, "write"))
+    except (subprocess.CalledProcessError, OSError) as err:
+        return None, f"counter pass failed: {err}"
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+
+    def ours(rows):
+        return [r for r in rows if "wo_" in r["Kernel_Name"] and "_kernel" in r["Kernel_Name"]]
+
+    def probe(rows, key):
+        hits = [float(r["Counter_Value"]) for r in rows if key(r["Kernel_Name"].lower())]
+        return max(hits) if hits else None
+    f_probe = probe(fetch, lambda n: "reduce" in n)   # the 256 MiB sum reads 256 MiB
+    w_probe = probe(write, lambda n: "fill" in n)     # the 256 MiB fill writes 256 MiB
+    fk, wk = ours(fetch), ours(write)
+    if not fk or len(fk) != len(wk) or not f_probe or not w_probe:
+        return None, "headline or calibration dispatches missing from the counter output"
+    f_scale = PROBE_BYTES / 1024 / f_probe
+    w_scale = PROBE_BYTES / 1024 / w_probe
+    per_m = {}
+    for i, (fr, wr) in enumerate(zip(fk, wk)):
+        M = MS[i % len(MS)]
+        per_m.setdefault(M, []).append((float(fr["Counter_Value"]) * f_scale + float(wr["Counter_Value"]) * w_scale) * 1024)
+    means = {M: sum(v) / len(v) for M, v in per_m.items()}
+    return {"bytes_per_launch": round(sum(means.values()) / len(means)),
+            "per_M_bytes": {f"M={M}": round(v) for M, v in sorted(means.items())},
+            "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
+            "dispatches": len(fk)}, None
 
 
 def main():
@@ -317,15 +504,23 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
+    ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--only", choices=["headline", "all"], default="all")
-    ap.add_argument("--copy-probe", action="store_true",
-                    help="also run a 256 MiB fill and a 256 MiB sum (the reference kernels for scaling "
-                         "rocprofv3 WRITE_SIZE / FETCH_SIZE readings to bytes)")
     args = ap.parse_args()
+    if args.traffic_child:
+        traffic_child()
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the quantized path has no multi-GPU code (every GPU box "
               "here has one GPU); run it with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    # the counter passes run as child processes before this process initialises the GPU
+    traffic, traffic_note = (None, "skipped (--no-traffic)")
+    if not args.no_traffic:
+        log("[bench] HBM traffic: rocprofv3 FETCH_SIZE / WRITE_SIZE passes")
+        traffic, traffic_note = measure_traffic()
+        log(f"[bench]   {traffic or traffic_note}")
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
@@ -338,19 +533,13 @@ def main():
     cfg, step_bytes, t = bench_headline(dev, args.steps, args.warmup)
     del cfg
     torch.cuda.empty_cache()
-    if args.copy_probe:
-        # known-size reference kernels: a 256 MiB fill (writes 256 MiB) and a sum over it
-        # (reads 256 MiB); the buffer is 256 MiB, the same as the MALL, so a second 256 MiB
-        # fill in between evicts it before the sum
-        a = torch.empty(64 * 2 ** 20, dtype=torch.float32, device=dev).fill_(1.0)
-        b = torch.empty_like(a).fill_(2.0)
-        a.sum()
-        torch.cuda.synchronize()
-        del a, b
     ms_per_step = t / args.steps * 1e3
     value = step_bytes * args.steps / t / 1e9
     avg_kernel_us = t / (4 * args.steps) * 1e6
     breakdown = {}
+    cpu_fns = {"int4_w4a16_sym_per_M": None, "int8_w8a16_gate_up_per_M": cpu_int8, "fp8_prefill_gemm": cpu_fp8,
+               "paged_decode_fp8_kv": lambda: cpu_attention("fp8"), "paged_decode_int8_kv": lambda: cpu_attention("int8"),
+               "moe_int4_layer": cpu_moe}
     if args.only == "all":
         for name, fn in (("int4_w4a16_sym_per_M", lambda: per_m(int4_setup(dev), int4_launch, int4_bytes, dev)),
                          ("int4_w4a16_zero_point_per_M", lambda: bench_int4_asym(dev)),
@@ -365,8 +554,30 @@ def main():
             log(f"[bench]   {breakdown[name]}")
     cpu = None
     if not args.no_cpu:
-        log("[bench] cpu baseline")
-        cpu = cpu_baseline_headline()
+        torch.set_num_threads(len(os.sched_getaffinity(0)))
+        log("[bench] cpu baseline (headline)")
+        cpu = cpu_int4_headline()
+        log(f"[bench]   {cpu}")
+        if args.only == "all":
+            for name, fn in cpu_fns.items():
+                if fn is None:
+                    breakdown[name]["cpu_baseline"] = cpu
+                    continue
+                log(f"[bench] cpu baseline ({name})")
+                breakdown[name]["cpu_baseline"] = fn()
+                log(f"[bench]   {breakdown[name]['cpu_baseline']}")
+    roofline = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(value / HBM_PEAK_GBS, 4),
+                "traffic": traffic["bytes_per_launch"] if traffic else None,
+                "traffic_unit": "bytes per launch (HBM, rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)",
+                "algorithmic_bytes_per_launch": round(step_bytes / 4),
+                "kernel": "wo_tile_kernel<int4> (M=1, 8) and wo_panel_kernel<int4> (M=32, 64)",
+                "avg_kernel_us": round(avg_kernel_us, 3)}
+    if traffic:
+        roofline["traffic_per_M"] = traffic["per_M_bytes"]
+        roofline["traffic_calibration"] = {"fetch_scale": traffic["fetch_scale"], "write_scale": traffic["write_scale"]}
+    else:
+        roofline["traffic_note"] = traffic_note
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -382,11 +593,7 @@ def main():
         "data": "synthetic (seeded N(0,0.02) weights quantized on the device, N(0,1) activations)",
         "config": {"workload": "INT4 W4A16 decode GEMM, Qwen3-4B down_proj N=2560 K=9728, group 128 symmetric, "
                                "one step = M in {1,8,32,64}", "global_batch": list(MS), "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(value / HBM_PEAK_GBS, 4), "traffic": HEADLINE_TRAFFIC_BYTES,
-                     "traffic_unit": "bytes per launch", "algorithmic_bytes_per_launch": round(step_bytes / 4),
-                     "kernel": "wo_tile_kernel<KIND_INT4> (M=1, 8) and wo_stream_kernel<KIND_INT4> (M=32, 64)",
-                     "avg_kernel_us": round(avg_kernel_us, 3)},
+        "roofline": roofline,
         "cpu_baseline": cpu,
         "breakdown": breakdown,
     }

@@ -164,7 +164,7 @@ __device__ __forceinline__ void produce(const PanelParams& p, int rb, int s, int
       for (int h = 0; h < 2; ++h) {
         const int kp = ((d + lc2 - nsteps_v) >> 31) & wrok[t][h];
         const int off = ((wbase[t][h] + d * kStepBytes) & kp) | (kOut & ~kp);
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2 /* nt */);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0);  // default policy: the other activation groups re-read these lines from L2
         wq[d + h][t] = *reinterpret_cast<const uint4*>(&v);
       }
   // value of group e (0-based in the range) of tile t; 16-bit values start in the high half

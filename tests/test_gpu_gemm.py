@@ -282,3 +282,37 @@ def test_w4a16_elementwise_vs_reference_formula(M, symmetric):
     print(f"[bound] M={M} sym={symmetric}: max |kernel - reference| {diff.max().item():.4f}, "
           f"max of diff / bound {(diff / bound).max().item():.3f}", flush=True)
     assert (diff <= bound).all()
+
+
+@pytest.mark.parametrize("variant", ["default", "four_waves", "previous_family", "strided_y"])
+def test_fp8_gemm_kernel_variants(variant, miq_env):
+    """Every FP8 kernel the dispatcher can reach at the large-tile shapes: the 8-wavefront
+    256x192 kernel (default), its 4-wavefront layout (MIQ_FP8_WAVES=4), the previous
+    256x192 family (MIQ_FP8_OLD, also taken for an output whose row stride is not a
+    multiple of 8), and a strided output through the C ABI (ldy = N + 4)."""
+    from kernels import _lib as L
+    from kernels import quant_ops as ops
+    case(f"fp8 gemm variant {variant}")
+    if variant == "four_waves":
+        miq_env("MIQ_FP8_WAVES", "4")
+    if variant == "previous_family":
+        miq_env("MIQ_FP8_OLD", "1")
+    M, N, K = 1024, 1920, 2560
+    x = torch.randn(M, K, generator=gen(54)).to(torch.bfloat16)
+    w = make_w(N, K, 55)
+    xq, xs = O.fp8_quantize_activation(x)
+    wq = O.fp8_quantize(w)
+    want = O.fp8_scaled_mm(xq, xs, **wq)
+    if variant != "strided_y":
+        y = ops.fp8_gemm(xq.to(DEV), xs.to(DEV), wq["qweight"].to(DEV), wq["scale"].to(DEV))
+    else:
+        ldy = N + 4
+        buf = torch.full((M, ldy), -7.0, dtype=torch.bfloat16, device=DEV)
+        xd, wd = xq.to(DEV).contiguous(), wq["qweight"].to(DEV).contiguous()
+        xsd, wsd = xs.reshape(-1).float().to(DEV), wq["scale"].reshape(-1).float().to(DEV)
+        L.call("miq_fp8_gemm", L.ptr(xd), L.ptr(xsd), L.ptr(wd), L.ptr(wsd), L.ptr(buf), ldy, M, N, K,
+               L.stream(buf.device))
+        torch.cuda.synchronize()
+        assert (buf[:, N:] == -7.0).all()  # the padding columns are not written
+        y = buf[:, :N]
+    within(y, want)

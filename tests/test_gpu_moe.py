@@ -136,3 +136,27 @@ def test_fused_moe_fp32_routing_weights_vs_reference_loop(sym):
           f"{d_loop.max().item():.4f}, max |fused - loop| {(got - loop).abs().max().item():.4f}", flush=True)
     assert ((got - loop).abs() <= d_loop + 1e-2 + 2e-2 * loop.abs()).all()
     assert rel_error(got, exact) < 2e-2
+
+
+@pytest.mark.parametrize("T,H,I,E,k,sym", [(64, 2048, 1024, 64, 8, True), (5, 256, 128, 8, 2, False),
+                                             (33, 512, 256, 6, 3, True)])
+def test_fused_int4_moe_tiled_kernels(T, H, I, E, k, sym, miq_env):
+    """The tiled expert kernels (one workgroup per (tile, column block), taken for shapes
+    the streaming kernels do not cover; MIQ_MOE_TILED forces them) against the same
+    reference as the default path."""
+    from kernels.fused_moe import fused_moe_int4
+    miq_env("MIQ_MOE_TILED", "1")
+    case(f"fused int4 moe tiled T={T} H={H} I={I} E={E} k={k} sym={sym}")
+    g = torch.Generator().manual_seed(13)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
+    wdn = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)
+    qf = O.int4_quantize_symmetric if sym else O.int4_quantize
+    gu, dn = qf(wgu, 128), qf(wdn, 128)
+    hidden, w, idx = routed(T, H, E, k, seed=14)
+    want = MO.int4_experts_reference(hidden, gu, dn, w, idx)
+    got = fused_moe_int4(hidden.to(DEV), idx.to(DEV), w.to(DEV), gu["qweight"].to(DEV), gu["scale"].to(DEV),
+                         None if sym else gu["zero"].to(DEV), dn["qweight"].to(DEV), dn["scale"].to(DEV),
+                         None if sym else dn["zero"].to(DEV))
+    assert rel_error(got, want) < 2e-2
+    err = (got.float().cpu() - want).abs()
+    assert (err <= 1e-2 + 2e-2 * want.abs()).all(), err.max().item()
