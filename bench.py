@@ -312,6 +312,35 @@ def bench_moe(dev):
     return res
 
 
+def bench_moe_int8(dev):
+    """Config 5's layer with INT8 experts (per-row scales), the fused INT8 path."""
+    from kernels import quant_ops as ops
+    from kernels.fused_moe import fused_moe_int8
+    T, H, inter, E, k = 64, 2048, 1024, 64, 8
+    hidden, w, idx = moe_routing(T, H, E, k)
+    hidden, w, idx = hidden.to(dev), w.to(dev), idx.to(dev)
+    dg = torch.Generator(device=dev).manual_seed(9)
+    wgu = (torch.randn(E, 2 * inter, H, generator=dg, device=dev) * 0.02).to(torch.bfloat16)
+    wdn = (torch.randn(E, H, inter, generator=dg, device=dev) * 0.02).to(torch.bfloat16)
+    gu = ops.int8_quantize(wgu, torch.bfloat16)
+    dn = ops.int8_quantize(wdn, torch.bfloat16)
+    del wgu, wdn
+    touched = int(idx.unique().numel())
+    per_expert = 2 * inter * H + H * inter + (2 * inter + H) * 2
+    nbytes = touched * per_expert + T * H * 2 * 2 + T * k * 6
+    n = copies_for(E * per_expert, 2)
+    sets = [(gu[0].clone(), gu[1].clone(), dn[0].clone(), dn[1].clone()) for _ in range(n)]
+
+    def launch(i):
+        gq, gs, dq, ds = sets[i % len(sets)]
+        return lambda: fused_moe_int8(hidden, idx, w, gq, gs, dq, ds)
+    reps = 8
+    t = time_graph([launch(i) for i in range(reps)]) / reps
+    gbs = nbytes / t / 1e9
+    return {"us_per_layer": round(t * 1e6, 2), "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+            "experts_touched": touched, "MB_per_call": round(nbytes / 1e6, 1)}
+
+
 # ---------------------------------------------------------------- CPU baselines (oracle)
 # The reference's CPU path restated in oracle/ (plain PyTorch), on the host cores of the
 # GPU box, at each configuration's shape; a bounded sample: whole calls until about
@@ -547,7 +576,8 @@ def main():
                          ("fp8_prefill_gemm", lambda: bench_fp8(dev)),
                          ("paged_decode_fp8_kv", lambda: bench_attention(dev, "fp8")),
                          ("paged_decode_int8_kv", lambda: bench_attention(dev, "int8")),
-                         ("moe_int4_layer", lambda: bench_moe(dev))):
+                         ("moe_int4_layer", lambda: bench_moe(dev)),
+                         ("moe_int8_layer", lambda: bench_moe_int8(dev))):
             log(f"[bench] {name}")
             breakdown[name] = fn()
             torch.cuda.empty_cache()

@@ -208,6 +208,21 @@ int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E
                   const int32_t* num_padded, void* workspace, size_t workspace_bytes,
                   void* out, void* stream);
 
+/* Replaces QuantExperts.forward (engine/quantization/modules.py:55-75) for Int8WeightOnly
+ * experts with a SiLU gate: the same layer as miq_w4a16_moe on int8 weights.
+ * gate_up q: int8 [E, 2I, H], scale [E, 2I] (or [E, 2I, 1]); down q: int8 [E, H, I],
+ * scale [E, H]; scale_dtype bf16 / f16 / f32. Each expert linear is int8_wo.linear's
+ * bf16(bf16(x @ q^T) * bf16(scale)) (int8_wo.py:17-21); the rest (SiLU gate, routing
+ * weight, expert-ordered bf16 combine) as miq_w4a16_moe. H and I multiples of 128;
+ * sorted_ids / expert_ids / num_padded from miq_moe_align with block_m == 16; workspace
+ * from miq_moe_workspace_bytes. out: bf16 [T, H]. */
+int miq_w8a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
+                  const int8_t* gu_q, const void* gu_scale, const int8_t* dn_q, const void* dn_scale,
+                  int scale_dtype, const void* topk_weights, int w_dtype,
+                  const int32_t* sorted_ids, const int32_t* expert_ids,
+                  const int32_t* num_padded, void* workspace, size_t workspace_bytes,
+                  void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -363,19 +363,22 @@ constexpr int kMoeChunk = 16;  // k-steps of activations staged at once
 #endif
 constexpr int kItemsPerRun = MIQ_MOE_RUN;  // consecutive items per workgroup (one staging)
 
-template <int MODE, bool HZ, int SD, bool G1>
+template <int KIND, int MODE, bool HZ, int SD, bool G1>
 __global__ void __launch_bounds__(256)
 moe_stream_kernel(MoeParams p, int blocks_per_tile) {
   extern __shared__ __align__(16) uint16_t lds[];
   __shared__ int s_src[kTile];
-  constexpr int NR = 2, NL = 1, D = kMoeD;
+  // int8 experts: a k-step of a tile is two 128-byte line loads (rows 0-7 and 8-15), the
+  // activations stay in natural order and one per-row scale is applied at the end
+  constexpr bool I8 = KIND == KIND_INT8;
+  constexpr int NR = 2, NL = I8 ? 2 : 1, D = kMoeD;
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
   const int K = MODE == MOE_GU ? p.H : p.I;
   const int steps = K / kStepK;
-  const int64_t ldw = K / 2;
+  const int64_t ldw = I8 ? K : K / 2;
   const int rows_per_expert = MODE == MOE_GU ? 2 * p.I : p.H;
-  const int64_t ngroups = steps / p.group_steps;
+  const int64_t ngroups = I8 ? 1 : steps / p.group_steps;
   const uint16_t* xbase = MODE == MOE_GU ? p.hidden : p.hbuf;
   const int ldx = K;
   const int npad = *p.num_padded;
@@ -432,11 +435,20 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
     }
     uint4 wq[D][NR][NL];
     uint32_t sq[D][NR], zq[D][NR];
-    static_assert(D % 2 == 0, "weight loads come in pairs of k-steps");
+    static_assert(I8 || D % 2 == 0, "int4 weight loads come in pairs of k-steps");
     auto request = [&](int d, int kl) {
       const int keep = (kl - nsteps_v) >> 31;
 #pragma unroll
       for (int t = 0; t < NR; ++t) {
+        if constexpr (I8) {
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int off = ((woff[t][h] + kl * 128) & keep) | (kOut & ~keep);
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2 /* nt */);
+            wq[d][t][h] = *reinterpret_cast<const uint4*>(&v);
+          }
+          continue;
+        }
         if ((d & 1) == 0) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
@@ -446,7 +458,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
             wq[d + h][t][0] = *reinterpret_cast<const uint4*>(&v);
           }
         }
-        const int gi = soff[t] + kl / p.group_steps;
+        const int gi = soff[t] + kl / p.group_steps;  // (int4 only past here)
         const int so = ((gi * esz) & ~3 & keep) | (kOut & ~keep);
         sq[d][t] = __builtin_amdgcn_raw_buffer_load_b32(srs, so, 0, 0);
         zq[d][t] = HZ ? __builtin_amdgcn_raw_buffer_load_b32(zrs, so, 0, 0) : 0u;
@@ -464,7 +476,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
     // Per quantization group, T = sum_k x (128 + u) + kXBias * sum_k x (MFMA chains and the
     // staged sums, which hold kXBias times the sum of x over each k-step), and
     // acc += s * T (+ z * sum_k x with zero points)
-    constexpr float kXBias = HZ ? -128.f : -136.f;
+    constexpr float kXBias = HZ || I8 ? -128.f : -136.f;
     f32x4 acc[NR], accg[NR], xsg;
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -492,7 +504,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
           const int i = base + tid + j * 256;
           const int ic = min(i, npieces - 1);
           const int m = ic / xcols, c = ic - m * xcols;
-          *reinterpret_cast<uint4*>(lds + m * xstride + c * 8) = permute_for_u4(xr[j]);
+          *reinterpret_cast<uint4*>(lds + m * xstride + c * 8) = I8 ? xr[j] : permute_for_u4(xr[j]);
           float sm = sum8_bf16(xr[j]);
           sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x111, 0xf, 0xf, true));
           sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x112, 0xf, 0xf, true));
@@ -511,11 +523,29 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
             bf16x8 av[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-              const uint4 v = *reinterpret_cast<const uint4*>(arow + a_off<KIND_INT4>(kl, g, j));
+              const uint4 v = *reinterpret_cast<const uint4*>(arow + a_off<KIND>(kl, g, j));
               av[j] = as_bf16x8(v.x, v.y, v.z, v.w);
             }
             const f32x4 xb = *reinterpret_cast<const f32x4*>(xsum + kl * kTile + g * 4);
             if (!G1) xsg += xb;
+            if constexpr (I8) {
+              // two MFMA chains per tile (even j into accg, odd j into acc); the +128 code
+              // offset leaves with -128 * sum x after the K loop
+#pragma unroll
+              for (int t = 0; t < NR; ++t) {
+                uint4 wl[2];
+                lanes_to_mfma(bp_addr, wq[d][t][0], wq[d][t][1], wl[0], wl[1]);
+                bf16x8 bv[4];
+                unpack_b<KIND_INT8>(wl, bv);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                  f32x4& chain = (j & 1) ? acc[t] : accg[t];
+                  chain = mfma(av[j], bv[j], chain);
+                }
+              }
+              request(d, kst + D);
+              continue;
+            }
 #pragma unroll
             for (int t = 0; t < NR; ++t) {
               bf16x8 bv[4];
@@ -569,6 +599,15 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
       }
     }
 
+    if constexpr (I8) {
+      // int8_wo.linear's result: bf16(bf16(x @ q^T) * bf16(scale)) per row (int8_wo.py:17-21)
+#pragma unroll
+      for (int t = 0; t < NR; ++t) {
+        const float sc = bf16r(sd_to_f32<SD>(load_sd_raw<SD>(sbase, row[t])));
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[t][v] = bf16r(bf16r(accg[t][v] + acc[t][v] + xsg[v]) * sc);
+      }
+    }
     // epilogue: lane (r, g) holds rows m = 4 g + v of columns r of both tiles
     if (MODE == MOE_GU) {
       const int col = blk * 64 + wv * 16 + r;
@@ -597,7 +636,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
   }
 }
 
-template <bool HZ, int SD, bool G1>
+template <int KIND, bool HZ, int SD, bool G1>
 void launch_stream_experts_g(const MoeParams& p, int max_tiles, hipStream_t st) {
   const int steps_gu = p.H / kStepK, steps_dn = p.I / kStepK;
   const size_t lds_gu = (size_t)kTile * (kMoeChunk * kStepK + 8) * 2 + (size_t)kMoeChunk * kTile * 4;
@@ -607,21 +646,21 @@ void launch_stream_experts_g(const MoeParams& p, int max_tiles, hipStream_t st) 
   // the LDS limit is set once per kernel (thread-safe)
   static std::once_flag lds_once;
   std::call_once(lds_once, [&] {
-    allow_max_dynamic_lds(reinterpret_cast<const void*>(&moe_stream_kernel<MOE_GU, HZ, SD, G1>));
-    allow_max_dynamic_lds(reinterpret_cast<const void*>(&moe_stream_kernel<MOE_DN, HZ, SD, G1>));
+    allow_max_dynamic_lds(reinterpret_cast<const void*>(&moe_stream_kernel<KIND, MOE_GU, HZ, SD, G1>));
+    allow_max_dynamic_lds(reinterpret_cast<const void*>(&moe_stream_kernel<KIND, MOE_DN, HZ, SD, G1>));
   });
   // about two workgroups per CU, never more than the runs of items that could exist
   const int grid_gu = std::max(1, std::min(512, max_tiles * bgu / kItemsPerRun));
   const int grid_dn = std::max(1, std::min(512, max_tiles * bdn / kItemsPerRun));
-  hipLaunchKernelGGL((moe_stream_kernel<MOE_GU, HZ, SD, G1>), dim3(grid_gu), dim3(256), lds_gu, st, p, bgu);
-  hipLaunchKernelGGL((moe_stream_kernel<MOE_DN, HZ, SD, G1>), dim3(grid_dn), dim3(256), lds_gu, st, p, bdn);
+  hipLaunchKernelGGL((moe_stream_kernel<KIND, MOE_GU, HZ, SD, G1>), dim3(grid_gu), dim3(256), lds_gu, st, p, bgu);
+  hipLaunchKernelGGL((moe_stream_kernel<KIND, MOE_DN, HZ, SD, G1>), dim3(grid_dn), dim3(256), lds_gu, st, p, bdn);
 }
 
 // one-step (128-code) groups have their own instantiation
 template <bool HZ, int SD>
 void launch_stream_experts(const MoeParams& p, int max_tiles, hipStream_t st) {
-  if (p.group_steps == 1) launch_stream_experts_g<HZ, SD, true>(p, max_tiles, st);
-  else launch_stream_experts_g<HZ, SD, false>(p, max_tiles, st);
+  if (p.group_steps == 1) launch_stream_experts_g<KIND_INT4, HZ, SD, true>(p, max_tiles, st);
+  else launch_stream_experts_g<KIND_INT4, HZ, SD, false>(p, max_tiles, st);
 }
 
 // out[t][n] = the sum of the token's pair outputs ypair[t * k + j][n] taken in the order of
@@ -723,30 +762,33 @@ extern "C" size_t miq_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, in
   return ((hb + 255) / 256) * 256 + ((yb + 255) / 256) * 256 + (size_t)T * topk * 4;
 }
 
-extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
-                             const uint8_t* gu_q, const void* gu_scale, const void* gu_zero,
-                             const uint8_t* dn_q, const void* dn_scale, const void* dn_zero,
-                             int sz_dtype, int64_t group, const void* topk_weights, int w_dtype,
-                             const int32_t* sorted_ids, const int32_t* expert_ids,
-                             const int32_t* num_padded, void* workspace, size_t workspace_bytes,
-                             void* out, void* stream) {
-  MIQ_REQUIRE(sz_dtype == MIQ_F32 || sz_dtype == MIQ_BF16 || sz_dtype == MIQ_F16, "w4a16_moe: bad scale dtype");
-  MIQ_REQUIRE(w_dtype == MIQ_F32 || w_dtype == MIQ_BF16 || w_dtype == MIQ_F16, "w4a16_moe: bad routing weight dtype");
-  MIQ_REQUIRE(topk <= kMaxCombineK, "w4a16_moe: topk=%lld above %d", (long long)topk, kMaxCombineK);
-  MIQ_REQUIRE(group >= kStepK && group % kStepK == 0 && H % group == 0 && I % group == 0,
-              "w4a16_moe: group=%lld must be a multiple of 128 dividing H and I", (long long)group);
+namespace {
+// Argument checks, workspace layout and launches shared by the INT4 and INT8 entry points.
+int run_moe(int kind, const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
+            const uint8_t* gu_q, const void* gu_scale, const void* gu_zero, const uint8_t* dn_q,
+            const void* dn_scale, const void* dn_zero, int sz_dtype, int64_t group, const void* topk_weights,
+            int w_dtype, const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* num_padded,
+            void* workspace, size_t workspace_bytes, void* out, void* stream, const char* name) {
+  const bool i8 = kind == KIND_INT8;
+  MIQ_REQUIRE(sz_dtype == MIQ_F32 || sz_dtype == MIQ_BF16 || sz_dtype == MIQ_F16, "%s: bad scale dtype", name);
+  MIQ_REQUIRE(w_dtype == MIQ_F32 || w_dtype == MIQ_BF16 || w_dtype == MIQ_F16, "%s: bad routing weight dtype", name);
+  MIQ_REQUIRE(topk <= kMaxCombineK, "%s: topk=%lld above %d", name, (long long)topk, kMaxCombineK);
+  MIQ_REQUIRE(i8 || (group >= kStepK && group % kStepK == 0 && H % group == 0 && I % group == 0),
+              "%s: group=%lld must be a multiple of 128 dividing H and I", name, (long long)group);
+  MIQ_REQUIRE(!i8 || (H % 128 == 0 && I % 128 == 0), "%s: H and I must be multiples of 128", name);
   MIQ_REQUIRE(H % 64 == 0 && I % 32 == 0 && T >= 1 && topk >= 1 && E >= 1 && H < (1 << 20) && I < (1 << 20),
-              "w4a16_moe: H must be a multiple of 64 and I of 32");
-  MIQ_REQUIRE((gu_zero == nullptr) == (dn_zero == nullptr), "w4a16_moe: zero points for both or neither");
+              "%s: H must be a multiple of 64 and I of 32", name);
+  MIQ_REQUIRE((gu_zero == nullptr) == (dn_zero == nullptr), "%s: zero points for both or neither", name);
   MIQ_REQUIRE(((reinterpret_cast<uintptr_t>(hidden) | reinterpret_cast<uintptr_t>(gu_q) |
                 reinterpret_cast<uintptr_t>(dn_q)) & 15) == 0,
-              "w4a16_moe: hidden and weights must be 16-byte aligned");
-  MIQ_REQUIRE(E * 2 * I * (H / 2) < 0x7fff0000LL && E * H * (I / 2) < 0x7fff0000LL,
-              "w4a16_moe: expert weights above 2 GiB");
+              "%s: hidden and weights must be 16-byte aligned", name);
+  const int64_t wdiv = i8 ? 1 : 2;
+  MIQ_REQUIRE(E * 2 * I * (H / wdiv) < 0x7fff0000LL && E * H * (I / wdiv) < 0x7fff0000LL,
+              "%s: expert weights above 2 GiB", name);
   const size_t need = miq_moe_workspace_bytes(T, topk, E, H, I);
-  MIQ_REQUIRE(workspace != nullptr && workspace_bytes >= need, "w4a16_moe: workspace of %zu bytes needed", need);
+  MIQ_REQUIRE(workspace != nullptr && workspace_bytes >= need, "%s: workspace of %zu bytes needed", name, need);
   MIQ_REQUIRE(((reinterpret_cast<uintptr_t>(workspace) & 15) | (reinterpret_cast<uintptr_t>(out) & 7)) == 0,
-              "w4a16_moe: workspace must be 16-byte and out 8-byte aligned");
+              "%s: workspace must be 16-byte and out 8-byte aligned", name);
   MoeParams p{};
   p.hidden = static_cast<const uint16_t*>(hidden);
   p.T = (int)T;
@@ -762,7 +804,7 @@ extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I
   p.dn_s = dn_scale;
   p.dn_z = dn_zero;
   p.sz_dtype = sz_dtype;
-  p.group_steps = (int)(group / kStepK);
+  p.group_steps = i8 ? 1 : (int)(group / kStepK);
   p.topk_w = topk_weights;
   p.w_dtype = w_dtype;
   p.sorted_ids = sorted_ids;
@@ -776,18 +818,48 @@ extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I
   p.out = static_cast<uint16_t*>(out);
   const unsigned tiles = (unsigned)((max_rows + kTile - 1) / kTile);
   hipStream_t st = (hipStream_t)stream;
-  // LDS chunk: 16 rows x up to 1024 k (32 KiB)
-  const int gu_chunk = (int)std::min<int64_t>(8, H / kStepK);
-  const int dn_chunk = (int)std::min<int64_t>(8, I / kStepK);
-  const size_t gu_lds = (size_t)kTile * (gu_chunk * kStepK + 8) * 2 + (size_t)64 * (H / group) * 4 * 2 +
-                        (size_t)kTile * (H / group) * 4;
-  const size_t dn_lds = (size_t)kTile * (dn_chunk * kStepK + 8) * 2 + (size_t)64 * (I / group) * 4 * 2 +
-                        (size_t)kTile * (I / group) * 4;
-  const dim3 gu_grid((unsigned)(I / 32), tiles), dn_grid((unsigned)(H / 64), tiles);
-  launch_experts(p, gu_zero != nullptr, sz_dtype, gu_grid, dn_grid, gu_chunk, dn_chunk, gu_lds, dn_lds, st);
-  int rc = check_launch("w4a16_moe experts");
+  if (i8) {
+    if (sz_dtype == MIQ_BF16) launch_stream_experts_g<KIND_INT8, false, MIQ_BF16, false>(p, (int)tiles, st);
+    else if (sz_dtype == MIQ_F16) launch_stream_experts_g<KIND_INT8, false, MIQ_F16, false>(p, (int)tiles, st);
+    else launch_stream_experts_g<KIND_INT8, false, MIQ_F32, false>(p, (int)tiles, st);
+  } else {
+    // LDS chunk: 16 rows x up to 1024 k (32 KiB)
+    const int gu_chunk = (int)std::min<int64_t>(8, H / kStepK);
+    const int dn_chunk = (int)std::min<int64_t>(8, I / kStepK);
+    const size_t gu_lds = (size_t)kTile * (gu_chunk * kStepK + 8) * 2 + (size_t)64 * (H / group) * 4 * 2 +
+                          (size_t)kTile * (H / group) * 4;
+    const size_t dn_lds = (size_t)kTile * (dn_chunk * kStepK + 8) * 2 + (size_t)64 * (I / group) * 4 * 2 +
+                          (size_t)kTile * (I / group) * 4;
+    const dim3 gu_grid((unsigned)(I / 32), tiles), dn_grid((unsigned)(H / 64), tiles);
+    launch_experts(p, gu_zero != nullptr, sz_dtype, gu_grid, dn_grid, gu_chunk, dn_chunk, gu_lds, dn_lds, st);
+  }
+  int rc = check_launch(name);
   if (rc) return rc;
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T), dim3(256), 0, st,
                      p.ypair, p.rank, (int)topk, (int)H, p.out);
-  return check_launch("w4a16_moe combine");
+  return check_launch(name);
+}
+}  // namespace
+
+extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
+                             const uint8_t* gu_q, const void* gu_scale, const void* gu_zero,
+                             const uint8_t* dn_q, const void* dn_scale, const void* dn_zero,
+                             int sz_dtype, int64_t group, const void* topk_weights, int w_dtype,
+                             const int32_t* sorted_ids, const int32_t* expert_ids,
+                             const int32_t* num_padded, void* workspace, size_t workspace_bytes,
+                             void* out, void* stream) {
+  return run_moe(KIND_INT4, hidden, T, H, I, E, topk, gu_q, gu_scale, gu_zero, dn_q, dn_scale, dn_zero, sz_dtype,
+                 group, topk_weights, w_dtype, sorted_ids, expert_ids, num_padded, workspace, workspace_bytes, out,
+                 stream, "w4a16_moe");
+}
+
+extern "C" int miq_w8a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
+                             const int8_t* gu_q, const void* gu_scale, const int8_t* dn_q, const void* dn_scale,
+                             int scale_dtype, const void* topk_weights, int w_dtype,
+                             const int32_t* sorted_ids, const int32_t* expert_ids,
+                             const int32_t* num_padded, void* workspace, size_t workspace_bytes,
+                             void* out, void* stream) {
+  return run_moe(KIND_INT8, hidden, T, H, I, E, topk, reinterpret_cast<const uint8_t*>(gu_q), gu_scale, nullptr,
+                 reinterpret_cast<const uint8_t*>(dn_q), dn_scale, nullptr, scale_dtype, 0, topk_weights, w_dtype,
+                 sorted_ids, expert_ids, num_padded, workspace, workspace_bytes, out, stream, "w8a16_moe");
 }

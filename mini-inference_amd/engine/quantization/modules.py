@@ -5,8 +5,9 @@ are buffers named after the method's dict keys (`qweight`, `scale` and, for asym
 INT4, `zero`), prefixed `gate_up_` / `down_` for experts, so state dicts and cache files
 are interchangeable; `forward` signatures are the reference's.
 
-`QuantExperts.forward` (modules.py:55-75) takes the fused INT4 MoE kernels when the
-experts are INT4 with a SiLU gate on a ROCm device. Otherwise it groups the (token, slot)
+`QuantExperts.forward` (modules.py:55-75) takes the fused MoE kernels when the experts
+are INT4 or INT8 with a SiLU gate on a ROCm device. Otherwise (FP8 experts, other gates,
+the CPU) it groups the (token, slot)
 pairs by expert with one sort and runs every hit expert through `method.linear`. The
 numerics are the reference loop's: gate/up and down in the compute dtype, the product
 with the routing weight in the weights' own dtype, and the results added in ascending
@@ -16,7 +17,8 @@ import torch
 from torch import nn
 
 from engine.quantization.int4_wo import Int4WeightOnly
-from kernels.fused_moe import fused_moe_int4
+from engine.quantization.int8_wo import Int8WeightOnly
+from kernels.fused_moe import fused_moe_int4, fused_moe_int8
 
 
 class _QuantTensors:
@@ -70,18 +72,28 @@ class QuantExperts(_QuantTensors, nn.Module):
         self._store("down_", down)
 
     def _fused_ok(self, hidden_states):
-        """The fused kernels' contract: INT4 codes in groups that are whole multiples of
-        128, bf16 activations on the device, SiLU gate, H and I multiples of the group."""
+        """The fused kernels' contract: bf16 activations on the device, a SiLU gate, and INT4
+        codes in groups that are whole multiples of 128 dividing H and I, or INT8 codes with
+        H and I multiples of 128."""
         m = self.method
-        if not isinstance(m, Int4WeightOnly) or hidden_states.device.type != "cuda":
+        if hidden_states.device.type != "cuda" or hidden_states.dtype != torch.bfloat16:
             return False
-        if hidden_states.dtype != torch.bfloat16 or not isinstance(self.act_fn, nn.SiLU):
+        if not isinstance(self.act_fn, nn.SiLU) or hidden_states.dim() != 2:
             return False
-        hidden, inter = hidden_states.shape[-1], self.down_qweight.shape[-1] * 2
-        return m.group_size % 128 == 0 and hidden % m.group_size == 0 and inter % m.group_size == 0
+        hidden = hidden_states.shape[-1]
+        if isinstance(m, Int4WeightOnly):
+            inter = self.down_qweight.shape[-1] * 2
+            return m.group_size % 128 == 0 and hidden % m.group_size == 0 and inter % m.group_size == 0
+        if isinstance(m, Int8WeightOnly):
+            inter = self.down_qweight.shape[-1]
+            return hidden % 128 == 0 and inter % 128 == 0
+        return False
 
     def forward(self, hidden_states, top_k_index, top_k_weights):
         if self._fused_ok(hidden_states):
+            if isinstance(self.method, Int8WeightOnly):
+                return fused_moe_int8(hidden_states, top_k_index, top_k_weights, self.gate_up_qweight,
+                                      self.gate_up_scale, self.down_qweight, self.down_scale)
             return fused_moe_int4(hidden_states, top_k_index, top_k_weights,
                                   self.gate_up_qweight, self.gate_up_scale, getattr(self, "gate_up_zero", None),
                                   self.down_qweight, self.down_scale, getattr(self, "down_zero", None))

@@ -53,6 +53,8 @@ SIGNATURES = {
                                 _P, _I64, _I64, _P]),
     "miq_moe_align": (_I32, [_P, _I32, _I64, _I64, _I64, _P, _P, _P, _P]),
     "miq_moe_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
+    "miq_w8a16_moe": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I32, _P, _I32, _P, _P, _P, _P, _SZ,
+                             _P, _P]),
     "miq_w4a16_moe": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I32, _I64, _P,
                              _I32, _P, _P, _P, _P, _SZ, _P, _P]),
 }

@@ -1,4 +1,4 @@
-"""Torch-facing wrappers of miq_moe_align and miq_w4a16_moe.
+"""Torch-facing wrappers of miq_moe_align, miq_w4a16_moe and miq_w8a16_moe.
 
 moe_align keeps the contract of the reference (kernels/fused_moe/fused_moe_triton.py:8-39
 and csrc/moe_align.cu:5-88): (sorted_ids, expert_ids, num_padded) with the pairs of each
@@ -57,4 +57,30 @@ def fused_moe_int4(hidden, topk_ids, topk_weights, gu_q, gu_scale, gu_zero, dn_q
            L.ptr(None if dn_zero is None else dn_zero.contiguous()),
            L.dtype_code(sdt), group, L.ptr(w), L.dtype_code(w.dtype), L.ptr(sorted_ids), L.ptr(expert_ids), L.ptr(num_padded),
            L.ptr(ws), nbytes, L.ptr(out), L.stream(hidden.device))
+    return out
+
+
+def fused_moe_int8(hidden, topk_ids, topk_weights, gu_q, gu_scale, dn_q, dn_scale):
+    """The INT8 twin of fused_moe_int4: every expert linear is int8_wo.linear
+    (bf16(bf16(x @ q^T) * bf16(scale)), int8_wo.py:17-21) and the rest of the layer is the
+    reference loop's (modules.py:55-75). gu_q int8 [E, 2I, H], gu_scale [E, 2I(, 1)];
+    dn_q int8 [E, H, I], dn_scale [E, H(, 1)]; both scales of one dtype."""
+    L.require_device(hidden, topk_ids, topk_weights, gu_q, dn_q, gu_scale, dn_scale)
+    T, H = hidden.shape
+    E, two_i, _ = gu_q.shape
+    inter = two_i // 2
+    k = topk_ids.shape[-1]
+    if dn_scale.dtype != gu_scale.dtype:
+        raise RuntimeError("fused_moe_int8: gate_up and down scales must share a dtype")
+    sorted_ids, expert_ids, num_padded = moe_align(topk_ids, E, BLOCK_M)
+    h = hidden.contiguous()
+    w = topk_weights.contiguous()
+    nbytes = L.load().miq_moe_workspace_bytes(T, k, E, H, inter)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=hidden.device)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=hidden.device)
+    gs, ds = gu_scale.contiguous(), dn_scale.contiguous()
+    L.call("miq_w8a16_moe", L.ptr(h), T, H, inter, E, k, L.ptr(gu_q.contiguous()), L.ptr(gs),
+           L.ptr(dn_q.contiguous()), L.ptr(ds), L.dtype_code(gs.dtype), L.ptr(w), L.dtype_code(w.dtype),
+           L.ptr(sorted_ids), L.ptr(expert_ids), L.ptr(num_padded), L.ptr(ws), nbytes, L.ptr(out),
+           L.stream(hidden.device))
     return out

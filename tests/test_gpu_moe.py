@@ -160,3 +160,56 @@ def test_fused_int4_moe_tiled_kernels(T, H, I, E, k, sym, miq_env):
     assert rel_error(got, want) < 2e-2
     err = (got.float().cpu() - want).abs()
     assert (err <= 1e-2 + 2e-2 * want.abs()).all(), err.max().item()
+
+
+@pytest.mark.parametrize("T,H,I,E,k", [(64, 2048, 1024, 64, 8), (5, 256, 128, 8, 2), (33, 512, 256, 6, 3),
+                                       (1, 2048, 1024, 64, 8)])
+@pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32])
+def test_fused_int8_moe_matches_reference_loop(T, H, I, E, k, wdtype):
+    """INT8 experts (Int8WeightOnly, per-row scales [E, rows, 1] in bf16): the fused layer
+    against the reference loop (modules.py:55-75) with the reference's own int8 linear
+    (int8_wo.py:17-21) on the same codes. Both round every expert linear, the SiLU gate,
+    the routing product and each addition to bf16 at the same points; they differ only in
+    fp32 summation order, so the elementwise bound is the north star's."""
+    from kernels.fused_moe import fused_moe_int8
+    case(f"fused int8 moe T={T} H={H} I={I} E={E} k={k} weights {wdtype}")
+    g = torch.Generator().manual_seed(15)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
+    wdn = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)
+    gu, dn = O.int8_quantize(wgu), O.int8_quantize(wdn)
+    hidden, w, idx = routed(T, H, E, k, seed=16)
+    if wdtype == torch.float32:
+        router = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16)
+        w = torch.softmax(hidden.float() @ router.float().t(), dim=-1).gather(1, idx)
+    loop = MO.quant_experts_loop(hidden, O.int8_linear, gu, dn, idx, w, E).float()
+    got = fused_moe_int8(hidden.to(DEV), idx.to(DEV), w.to(DEV), gu["qweight"].to(DEV), gu["scale"].to(DEV),
+                         dn["qweight"].to(DEV), dn["scale"].to(DEV)).float().cpu()
+    err = (got - loop).abs()
+    print(f"[bound] int8 moe T={T} {wdtype}: max |fused - reference loop| {err.max().item():.4f}", flush=True)
+    assert rel_error(got, loop) < 1e-2
+    assert (err <= 1e-2 + 2e-2 * loop.abs()).all(), err.max().item()
+
+
+def test_quant_experts_int8_takes_the_fused_path():
+    """QuantExperts with Int8WeightOnly on the device runs the fused kernels (no host loop)
+    and matches its own grouped per-expert path."""
+    from engine.quantization import get_method
+    from engine.quantization.modules import QuantExperts
+    case("QuantExperts int8 fused vs grouped")
+
+    class Experts(torch.nn.Module):
+        def __init__(self, E, H, I):
+            super().__init__()
+            g = torch.Generator().manual_seed(17)
+            self.gate_up_proj = torch.nn.Parameter((torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16))
+            self.down_proj = torch.nn.Parameter((torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16))
+            self.act_fn = torch.nn.SiLU()
+
+    E, H, I, T, k = 16, 512, 256, 24, 4
+    qe = QuantExperts(Experts(E, H, I).to(DEV), get_method("int8_wo", device=DEV))
+    hidden, w, idx = routed(T, H, E, k, seed=18)
+    hd, wd, idd = hidden.to(DEV), w.to(DEV), idx.to(DEV)
+    assert qe._fused_ok(hd)
+    fused = qe(hd, idd, wd)
+    grouped = qe._grouped(hd, idd, wd)
+    assert rel_error(fused, grouped) < 1e-2
