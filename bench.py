@@ -527,6 +527,18 @@ def measure_traffic():
             "dispatches": len(fk)}, None
 
 
+SECTIONS = {
+    "int4_w4a16_sym_per_M": lambda dev: per_m(int4_setup(dev), int4_launch, int4_bytes, dev),
+    "int4_w4a16_zero_point_per_M": bench_int4_asym,
+    "int8_w8a16_gate_up_per_M": bench_int8,
+    "fp8_prefill_gemm": bench_fp8,
+    "paged_decode_fp8_kv": lambda dev: bench_attention(dev, "fp8"),
+    "paged_decode_int8_kv": lambda dev: bench_attention(dev, "int8"),
+    "moe_int4_layer": bench_moe,
+    "moe_int8_layer": bench_moe_int8,
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -535,7 +547,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 counter passes")
     ap.add_argument("--traffic-child", action="store_true", help=argparse.SUPPRESS)
-    ap.add_argument("--only", choices=["headline", "all"], default="all")
+    ap.add_argument("--only", choices=["headline", "all"] + list(SECTIONS), default="all",
+                    help="headline: the headline line only; a section name: that configuration alone "
+                         "(for profiling runs; prints its breakdown entry)")
     args = ap.parse_args()
     if args.traffic_child:
         traffic_child()
@@ -557,6 +571,9 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.only in SECTIONS:
+        print(json.dumps({args.only: SECTIONS[args.only](dev)}), flush=True)
+        return
 
     log("[bench] headline: INT4 W4A16 decode GEMM sweep")
     cfg, step_bytes, t = bench_headline(dev, args.steps, args.warmup)
@@ -570,14 +587,8 @@ def main():
                "paged_decode_fp8_kv": lambda: cpu_attention("fp8"), "paged_decode_int8_kv": lambda: cpu_attention("int8"),
                "moe_int4_layer": cpu_moe}
     if args.only == "all":
-        for name, fn in (("int4_w4a16_sym_per_M", lambda: per_m(int4_setup(dev), int4_launch, int4_bytes, dev)),
-                         ("int4_w4a16_zero_point_per_M", lambda: bench_int4_asym(dev)),
-                         ("int8_w8a16_gate_up_per_M", lambda: bench_int8(dev)),
-                         ("fp8_prefill_gemm", lambda: bench_fp8(dev)),
-                         ("paged_decode_fp8_kv", lambda: bench_attention(dev, "fp8")),
-                         ("paged_decode_int8_kv", lambda: bench_attention(dev, "int8")),
-                         ("moe_int4_layer", lambda: bench_moe(dev)),
-                         ("moe_int8_layer", lambda: bench_moe_int8(dev))):
+        for name, fn in SECTIONS.items():
+            fn = (lambda f: (lambda: f(dev)))(fn)
             log(f"[bench] {name}")
             breakdown[name] = fn()
             torch.cuda.empty_cache()
