@@ -92,7 +92,9 @@ int miq_fp8_quantize_rows(const void* x, int x_dtype, int64_t rows, int64_t K, i
 int miq_fp8_dequantize(const uint8_t* q, const float* scale, int64_t rows, int64_t K,
                        float* out, void* stream);
 
-/* ------------------------------------------------------------------ skinny decode GEMMs
+/* ------------------------------------------------------------------ weight-only GEMMs
+ * Any M >= 1: decode kernels up to M = 64, a dequantize-in-the-K-loop MFMA GEMM above
+ * (prefill), which splits K when the output has fewer 64 x 128 tiles than CUs.
  * Workspace for the split-K reduction of the two weight-only GEMMs. Its first 16384
  * bytes hold arrival counters that must be zero before the first call (zero the whole
  * buffer once when allocating it); every call leaves them at zero again, and the fp32
@@ -103,7 +105,7 @@ size_t miq_wo_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_b
 /* Replaces Int8WeightOnly.linear (int8_wo.py:17-21):
  *   y = bf16( bf16(x @ q^T) * bf16(scale) )
  * x: bf16 [M, K] row stride ldx; q: int8 [N, K] contiguous; scale: [N] of scale_dtype;
- * y: bf16 [M, N] row stride ldy. 1 <= M <= 64, K % 128 == 0, N % 16 == 0. */
+ * y: bf16 [M, N] row stride ldy. M >= 1, K % 128 == 0, N % 16 == 0. */
 int miq_w8a16_gemm(const void* x, int64_t ldx, const int8_t* q, const void* scale,
                    int scale_dtype, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                    void* workspace, size_t workspace_bytes, void* stream);
@@ -112,7 +114,7 @@ int miq_w8a16_gemm(const void* x, int64_t ldx, const int8_t* q, const void* scal
  * (engine/quantization/base.py:20-24, int4_wo.py:33-42): y = bf16(x @ W^T) with
  * W = q * scale + zero (zero == NULL: W = (q - 8) * scale), evaluated in fp32 as
  * scale * (x . q) + zero * sum(x) per group. x: bf16 [M, K]; q: uint8 [N, K/2];
- * scale/zero: [N, K/group] of sz_dtype (bf16/f16/f32). 1 <= M <= 64, group % 128 == 0,
+ * scale/zero: [N, K/group] of sz_dtype (bf16/f16/f32). M >= 1, group % 128 == 0,
  * K % group == 0, N % 16 == 0. */
 int miq_w4a16_gemm(const void* x, int64_t ldx, const uint8_t* q, const void* scale,
                    const void* zero, int sz_dtype, int64_t group, void* y, int64_t ldy,

@@ -21,6 +21,11 @@ int wo_panel_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ld
                     int N, int K, void* workspace, size_t ws_bytes, size_t counter_bytes, hipStream_t st,
                     const char* name, bool& launched);
 constexpr size_t kWoCounterBytes = 16384;  // the workspace's counter area (4096 ints)
+size_t wo_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits, size_t counter_bytes);
+int wo_prefill_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, const void* scale,
+                      const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int64_t M,
+                      int N, int K, void* workspace, size_t ws_bytes, size_t counter_bytes, hipStream_t st,
+                      const char* name);
 int wo_tile_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, const void* scale,
                    const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int M,
                    int N, int K, hipStream_t st, const char* name, bool& launched);
@@ -45,13 +50,16 @@ struct WoArgs {
 };
 
 int run(int kind, const WoArgs& p, void* workspace, size_t ws_bytes, hipStream_t st, const char* name) {
-  MIQ_REQUIRE(p.M >= 1 && p.M <= 64, "%s: M=%d must be in [1, 64]", name, p.M);
+  MIQ_REQUIRE(p.M >= 1, "%s: M=%d must be positive", name, p.M);
   MIQ_REQUIRE(p.K % kStepK == 0 && p.K > 0, "%s: K=%d must be a multiple of 128", name, p.K);
   MIQ_REQUIRE(p.N % 16 == 0 && p.N > 0, "%s: N=%d must be a multiple of 16", name, p.N);
   MIQ_REQUIRE(p.ldx % 8 == 0 && (reinterpret_cast<uintptr_t>(p.x) & 15) == 0,
               "%s: x must be 16-byte aligned with a row stride multiple of 8", name);
   MIQ_REQUIRE((reinterpret_cast<uintptr_t>(p.w) & 15) == 0, "%s: weights must be 16-byte aligned", name);
   MIQ_REQUIRE(p.ldx >= p.K && p.ldy >= p.N, "%s: bad strides", name);
+  if (p.M > 64)  // prefill: the dequantize-in-the-K-loop MFMA GEMM
+    return wo_prefill_launch(kind, p.x, p.ldx, p.w, p.ldw, p.scale, p.zero, p.sz_dtype, p.group_steps, p.ngroups,
+                             p.y, p.ldy, p.M, p.N, p.K, workspace, ws_bytes, kWoCounterBytes, st, name);
   bool launched = false;
   if (kind == KIND_INT4) {
     const int rc = wo_panel_launch(p.x, p.ldx, p.w, p.ldw, p.scale, p.zero, p.sz_dtype, p.group_steps, p.ngroups,
@@ -72,6 +80,7 @@ int run(int kind, const WoArgs& p, void* workspace, size_t ws_bytes, hipStream_t
 using namespace miq;
 
 extern "C" size_t miq_wo_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits) {
+  if (M > 64 && N >= 1 && K >= kStepK) return std::max(kWoCounterBytes, wo_prefill_workspace_bytes(M, N, K, weight_bits, kWoCounterBytes));
   const size_t stream = wo_stream_workspace_bytes(M, N, K, weight_bits);
   if (weight_bits != 4 || M < 1 || M > 64 || N < 1 || K < kStepK) return stream;
   return std::max(stream, kWoCounterBytes + wo_panel_partial_bytes(M, N, K));
@@ -82,7 +91,7 @@ extern "C" int miq_w8a16_gemm(const void* x, int64_t ldx, const int8_t* q, const
                               void* workspace, size_t workspace_bytes, void* stream) {
   MIQ_REQUIRE(scale_dtype == MIQ_F32 || scale_dtype == MIQ_BF16 || scale_dtype == MIQ_F16,
               "w8a16_gemm: bad scale dtype");
-  MIQ_REQUIRE(N < (1LL << 30) && K < (1LL << 30), "w8a16_gemm: dims too large");
+  MIQ_REQUIRE(M < (1LL << 30) && N < (1LL << 30) && K < (1LL << 30), "w8a16_gemm: dims too large");
   WoArgs p{};
   p.x = static_cast<const uint16_t*>(x);
   p.ldx = ldx;
@@ -110,7 +119,7 @@ extern "C" int miq_w4a16_gemm(const void* x, int64_t ldx, const uint8_t* q, cons
   MIQ_REQUIRE(group >= kStepK && group % kStepK == 0 && K % group == 0,
               "w4a16_gemm: group=%lld must be a multiple of 128 dividing K=%lld", (long long)group,
               (long long)K);
-  MIQ_REQUIRE(N < (1LL << 30) && K < (1LL << 30), "w4a16_gemm: dims too large");
+  MIQ_REQUIRE(M < (1LL << 30) && N < (1LL << 30) && K < (1LL << 30), "w4a16_gemm: dims too large");
   WoArgs p{};
   p.x = static_cast<const uint16_t*>(x);
   p.ldx = ldx;

@@ -39,8 +39,10 @@ class Int4WeightOnly(QuantMethod):
     def linear(self, x, qweight, scale, zero=None):
         """base.py:20-24 with the int4 dequantize.
 
-        Decode-sized inputs run the fused skinny GEMM (unpack + scale inside the K loop);
-        larger inputs dequantize with the kernel and use the device GEMM."""
+        Up to kernels.quant_ops.PREFILL_MAX_M[4] rows the fused GEMM runs (unpack and scale
+        inside the K loop: the decode kernels up to 64 rows, the prefill kernel above);
+        larger inputs dequantize with the kernel and use the device GEMM, which is faster
+        there."""
         if ops.w4a16_supported(x, qweight, scale):
             return ops.w4a16_linear(x, qweight, scale, zero)
         w = self.dequantize(qweight, scale, zero).to(x.dtype)

@@ -24,9 +24,9 @@ class Int8WeightOnly(QuantMethod):
     def linear(self, x, qweight, scale):
         """int8_wo.py:17-21: (x @ q^T) * scale.
 
-        Decode-sized inputs (1..64 rows) run the fused skinny GEMM that reads the int8
-        weights once; larger inputs (prefill) use the reference's own formula with the
-        device GEMM."""
+        Up to kernels.quant_ops.PREFILL_MAX_M[8] rows the fused GEMM runs (the int8 codes
+        are read once, no bf16 weight is written); larger inputs use the reference's own
+        formula with the device GEMM, which is faster there."""
         if ops.w8a16_supported(x, qweight):
             return ops.w8a16_linear(x, qweight, scale)
         y = torch.nn.functional.linear(x, qweight.to(x.dtype))

@@ -10,7 +10,11 @@ import torch
 
 from kernels import _lib as L
 
-SKINNY_MAX_M = 64  # the weight-only GEMM kernels take 1..64 activation rows
+SKINNY_MAX_M = 64  # decode kernels up to 64 activation rows; above, the prefill kernel
+# Largest M for which the fused prefill kernel is used by the quantization methods; above it
+# the methods dequantize and call the device GEMM, which measured faster on MI355X from
+# about these sizes (INT4: M = 1536 at 2560 x 9728 and 19456 x 2560; INT8: M = 768).
+PREFILL_MAX_M = {4: 1024, 8: 512}
 
 
 def _rows(t):
@@ -51,7 +55,7 @@ def int8_dequantize(qweight, scale):
 
 
 def w8a16_linear(x, qweight, scale):
-    """int8_wo.py:17-21 for 1..64 rows: y = bf16(bf16(x @ q^T) * bf16(scale))."""
+    """int8_wo.py:17-21: y = bf16(bf16(x @ q^T) * bf16(scale)), any number of rows."""
     L.require_device(x, qweight, scale)
     K = x.shape[-1]
     N = qweight.shape[-2]
@@ -69,7 +73,7 @@ def w8a16_linear(x, qweight, scale):
 
 def w8a16_supported(x, qweight):
     M = _rows(x)
-    return (x.dtype == torch.bfloat16 and 1 <= M <= SKINNY_MAX_M and x.shape[-1] % 128 == 0
+    return (x.dtype == torch.bfloat16 and 1 <= M <= PREFILL_MAX_M[8] and x.shape[-1] % 128 == 0
             and qweight.shape[-2] % 16 == 0 and qweight.dim() == 2)
 
 
@@ -105,7 +109,7 @@ def int4_dequantize(qweight, scale, zero):
 
 
 def w4a16_linear(x, qweight, scale, zero):
-    """QuantMethod.linear over Int4WeightOnly (base.py:20-24) for 1..64 rows."""
+    """QuantMethod.linear over Int4WeightOnly (base.py:20-24), any number of rows."""
     L.require_device(x, qweight, scale, zero)
     K = x.shape[-1]
     N = qweight.shape[-2]
@@ -129,7 +133,7 @@ def w4a16_supported(x, qweight, scale):
     if scale.shape[-1] == 0 or K % scale.shape[-1]:
         return False
     group = K // scale.shape[-1]
-    return (x.dtype == torch.bfloat16 and 1 <= M <= SKINNY_MAX_M and group % 128 == 0
+    return (x.dtype == torch.bfloat16 and 1 <= M <= PREFILL_MAX_M[4] and group % 128 == 0
             and qweight.shape[-2] % 16 == 0 and qweight.dim() == 2)
 
 

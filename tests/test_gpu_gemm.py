@@ -316,3 +316,49 @@ def test_fp8_gemm_kernel_variants(variant, miq_env):
         assert (buf[:, N:] == -7.0).all()  # the padding columns are not written
         y = buf[:, :N]
     within(y, want)
+
+
+PREFILL_SHAPES = [(65, 256, 512, 128), (96, 320, 1152, 384), (200, 2560, 9728, 128), (130, 144, 2048, 1024),
+                  (257, 512, 1024, 256), (1300, 2560, 512, 128)]
+
+
+def workspace_is_zero():
+    """The split-K workspace is all zeros between calls (the decode kernels that share it
+    read a non-zero partial word as pending)."""
+    from kernels import _lib as L
+    torch.cuda.synchronize()
+    ws = L.wo_workspace(torch.device("cuda", torch.cuda.current_device()), 0)
+    return int(ws.count_nonzero().item()) == 0
+
+
+@pytest.mark.parametrize("M,N,K,group", PREFILL_SHAPES)
+@pytest.mark.parametrize("symmetric", [False, True])
+def test_w4a16_prefill(M, N, K, group, symmetric):
+    """M > 64 (prefill): the dequantize-in-the-K-loop MFMA GEMM, ragged M and N, groups of
+    1 to 8 k-steps, odd k-step counts."""
+    from kernels import quant_ops as ops
+    case(f"w4a16 prefill M={M} N={N} K={K} g={group} sym={symmetric}")
+    w = make_w(N, K, 80)
+    x = make_x(M, K, 81)
+    q = O.int4_quantize_symmetric(w, group) if symmetric else O.int4_quantize(w, group)
+    want = O.int4_linear_fp32(x, **q)
+    y = ops.w4a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV), None if symmetric else q["zero"].to(DEV))
+    assert y.shape == (M, N)
+    within(y, want)
+    assert workspace_is_zero()
+
+
+@pytest.mark.parametrize("M,N,K", [(65, 256, 512), (200, 19456, 2560), (129, 144, 1152), (300, 512, 2560),
+                                   (96, 2560, 9728)])
+@pytest.mark.parametrize("sdt", [torch.bfloat16, torch.float32])
+def test_w8a16_prefill(M, N, K, sdt):
+    from kernels import quant_ops as ops
+    case(f"w8a16 prefill M={M} N={N} K={K} {sdt}")
+    w = make_w(N, K, 82)
+    x = make_x(M, K, 83)
+    q = O.int8_quantize(w, sdt)
+    want = O.int8_linear_fp32(x, **q)
+    y = ops.w8a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV))
+    within(y, want)
+    assert rel(y, O.int8_linear(x, **q)) < 0.01
+    assert workspace_is_zero()
