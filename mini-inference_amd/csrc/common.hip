@@ -30,6 +30,10 @@ Tuning read_tuning() {
   t.wo_panel_mt = pm ? atoi(pm) : 0;
   const char* pa = getenv("MIQ_WO_PANEL_ABL");
   t.wo_panel_abl = pa ? atoi(pa) : 0;
+  const char* pmm = getenv("MIQ_WO_PREFILL_MIN_M");
+  t.wo_prefill_min_m = pmm && atoi(pmm) > 0 ? atoi(pmm) : 65;
+  const char* pps = getenv("MIQ_WO_PREFILL_S");
+  t.wo_prefill_s = pps ? atoi(pps) : 0;
   t.fp8_old = flag("MIQ_FP8_OLD");
   const char* fw = getenv("MIQ_FP8_WAVES");
   t.fp8_four_waves = fw && atoi(fw) == 4;

@@ -183,6 +183,8 @@ struct Tuning {
   int wo_panel_s;             // MIQ_WO_PANEL_S: K splits of the panel kernel (0: planned)
   int wo_panel_mt;            // MIQ_WO_PANEL_MT: activation tiles per panel workgroup (1, 2, 4)
   int wo_panel_abl;           // MIQ_WO_PANEL_ABL: ablation runs (timing only; wrong results)
+  int wo_prefill_min_m;       // MIQ_WO_PREFILL_MIN_M: smallest M for the prefill kernel (65)
+  int wo_prefill_s;           // MIQ_WO_PREFILL_S: K splits of the prefill kernel (0: planned)
   bool fp8_old;               // MIQ_FP8_OLD: the previous FP8 GEMM kernel family
   bool fp8_four_waves;        // MIQ_FP8_WAVES=4
   bool moe_tiled;             // MIQ_MOE_TILED: the tiled expert kernels

@@ -278,6 +278,10 @@ moe_gate_up_kernel(MoeParams p, int chunk_steps) {
   extern __shared__ __align__(16) uint16_t lds[];
   __shared__ int s_src[kTile];
   __shared__ float s_gu[4][kTile][16 + 1];
+  // every pair starts unranked (-1); the down kernel, which runs after this one, ranks the
+  // pairs routed to an expert
+  for (int i = (blockIdx.y * gridDim.x + blockIdx.x) * 256 + threadIdx.x; i < p.num_pairs; i += gridDim.x * gridDim.y * 256)
+    p.rank[i] = -1;
   const int tile = blockIdx.y;
   if (tile * kTile >= *p.num_padded) return;
   const int e = p.expert_ids[tile];
@@ -402,6 +406,8 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
   // the whole K fits one chunk its activations are staged once per run
   const bool one_chunk = steps <= kMoeChunk;
   int staged_tile = -1;
+  if (MODE == MOE_GU)  // every pair starts unranked (-1); the down kernel ranks the routed ones
+    for (int i = blockIdx.x * 256 + tid; i < p.num_pairs; i += gridDim.x * 256) p.rank[i] = -1;
   for (int k = 0;; ++k) {
     const int item = (blockIdx.x + (k / kItemsPerRun) * gridDim.x) * kItemsPerRun + k % kItemsPerRun;
     const int tile = item / blocks_per_tile, blk = item - tile * blocks_per_tile;
@@ -458,10 +464,14 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
             wq[d + h][t][0] = *reinterpret_cast<const uint4*>(&v);
           }
         }
+#ifdef MIQ_MOE_ABL_NOSCALE
+        sq[d][t] = 0x3c003c00u; zq[d][t] = 0u; (void)keep;
+#else
         const int gi = soff[t] + kl / p.group_steps;  // (int4 only past here)
         const int so = ((gi * esz) & ~3 & keep) | (kOut & ~keep);
         sq[d][t] = __builtin_amdgcn_raw_buffer_load_b32(srs, so, 0, 0);
         zq[d][t] = HZ ? __builtin_amdgcn_raw_buffer_load_b32(zrs, so, 0, 0) : 0u;
+#endif
       }
     };
     if (stage && tid < kTile) {
@@ -668,31 +678,47 @@ void launch_stream_experts(const MoeParams& p, int max_tiles, hipStream_t st) {
 // each expert's bf16 contribution into a bf16 output, expert after expert
 // (modules.py:55-75, index_add_). Four consecutive n per thread (H is a multiple of 64).
 constexpr int kMaxCombineK = 32;
+// KT >= topk slots, unrolled: all slot loads are issued at once (one memory round trip,
+// not one per slot), then the position of each slot in rank order is counted and the
+// values are added in that order. Ranks are distinct (they are sorted-pair indices); a
+// slot whose expert id was out of range has rank -1 and adds nothing, as in the loop
+// over experts, which skips such ids.
+template <int KT>
 __global__ void moe_combine_kernel(const uint16_t* __restrict__ ypair, const int32_t* __restrict__ rank, int topk,
                                    int H, uint16_t* __restrict__ out) {
   const int t = blockIdx.y;
   const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (n >= H) return;
-  // the slots of the token in rank order (k is small: a selection pass per slot)
-  int order[kMaxCombineK];
-  int last = -1;
-  for (int j = 0; j < topk; ++j) {
-    int best = -1, best_rank = 0x7fffffff;
-    for (int i = 0; i < topk; ++i) {
-      const int rk = rank[(int64_t)t * topk + i];
-      if (rk > last && rk < best_rank) { best_rank = rk; best = i; }
-    }
-    order[j] = best;
-    last = best_rank;
+  const uint16_t* row = ypair + (int64_t)t * topk * H + n;
+  int rk[KT];
+  uint2 v[KT];
+  int nvalid = 0;  // slots routed to an expert (rank >= 0; an out-of-range id keeps -1)
+#pragma unroll
+  for (int i = 0; i < KT; ++i) {
+    const int r = i < topk ? rank[(int64_t)t * topk + i] : -1;
+    rk[i] = r >= 0 ? r : 0x7fffffff;
+    nvalid += r >= 0 ? 1 : 0;
+    v[i] = r >= 0 ? *reinterpret_cast<const uint2*>(row + (int64_t)i * H) : make_uint2(0, 0);
+  }
+  int pos[KT];
+#pragma unroll
+  for (int i = 0; i < KT; ++i) {
+    int c = 0;
+#pragma unroll
+    for (int j = 0; j < KT; ++j) c += rk[j] < rk[i] ? 1 : 0;
+    pos[i] = c;
   }
   float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-  const uint16_t* row = ypair + (int64_t)t * topk * H + n;
-  for (int j = 0; j < topk; ++j) {
-    const uint2 v = *reinterpret_cast<const uint2*>(row + (int64_t)order[j] * H);
-    s.x = bf16r(s.x + __builtin_bit_cast(float, v.x << 16));
-    s.y = bf16r(s.y + __builtin_bit_cast(float, v.x & 0xffff0000u));
-    s.z = bf16r(s.z + __builtin_bit_cast(float, v.y << 16));
-    s.w = bf16r(s.w + __builtin_bit_cast(float, v.y & 0xffff0000u));
+#pragma unroll
+  for (int q = 0; q < KT; ++q) {
+    if (q >= nvalid) break;
+    uint2 w = make_uint2(0, 0);
+#pragma unroll
+    for (int i = 0; i < KT; ++i) w = pos[i] == q ? v[i] : w;
+    s.x = bf16r(s.x + __builtin_bit_cast(float, w.x << 16));
+    s.y = bf16r(s.y + __builtin_bit_cast(float, w.x & 0xffff0000u));
+    s.z = bf16r(s.z + __builtin_bit_cast(float, w.y << 16));
+    s.w = bf16r(s.w + __builtin_bit_cast(float, w.y & 0xffff0000u));
   }
   const uint32_t lo = f32_to_bf16(s.x) | ((uint32_t)f32_to_bf16(s.y) << 16);
   const uint32_t hi = f32_to_bf16(s.z) | ((uint32_t)f32_to_bf16(s.w) << 16);
@@ -835,8 +861,13 @@ int run_moe(int kind, const void* hidden, int64_t T, int64_t H, int64_t I, int64
   }
   int rc = check_launch(name);
   if (rc) return rc;
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)T), dim3(256), 0, st,
-                     p.ypair, p.rank, (int)topk, (int)H, p.out);
+  const dim3 cgrid((unsigned)((H / 4 + 255) / 256), (unsigned)T);
+  if (topk <= 8)
+    hipLaunchKernelGGL(moe_combine_kernel<8>, cgrid, dim3(256), 0, st, p.ypair, p.rank, (int)topk, (int)H, p.out);
+  else if (topk <= 16)
+    hipLaunchKernelGGL(moe_combine_kernel<16>, cgrid, dim3(256), 0, st, p.ypair, p.rank, (int)topk, (int)H, p.out);
+  else
+    hipLaunchKernelGGL(moe_combine_kernel<32>, cgrid, dim3(256), 0, st, p.ypair, p.rank, (int)topk, (int)H, p.out);
   return check_launch(name);
 }
 }  // namespace

@@ -57,7 +57,7 @@ int run(int kind, const WoArgs& p, void* workspace, size_t ws_bytes, hipStream_t
               "%s: x must be 16-byte aligned with a row stride multiple of 8", name);
   MIQ_REQUIRE((reinterpret_cast<uintptr_t>(p.w) & 15) == 0, "%s: weights must be 16-byte aligned", name);
   MIQ_REQUIRE(p.ldx >= p.K && p.ldy >= p.N, "%s: bad strides", name);
-  if (p.M > 64)  // prefill: the dequantize-in-the-K-loop MFMA GEMM
+  if (p.M >= tuning().wo_prefill_min_m)  // prefill (M > 64): the dequantize-in-the-K-loop MFMA GEMM
     return wo_prefill_launch(kind, p.x, p.ldx, p.w, p.ldw, p.scale, p.zero, p.sz_dtype, p.group_steps, p.ngroups,
                              p.y, p.ldy, p.M, p.N, p.K, workspace, ws_bytes, kWoCounterBytes, st, name);
   bool launched = false;
@@ -80,10 +80,12 @@ int run(int kind, const WoArgs& p, void* workspace, size_t ws_bytes, hipStream_t
 using namespace miq;
 
 extern "C" size_t miq_wo_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits) {
-  if (M > 64 && N >= 1 && K >= kStepK) return std::max(kWoCounterBytes, wo_prefill_workspace_bytes(M, N, K, weight_bits, kWoCounterBytes));
+  const size_t prefill = M >= tuning().wo_prefill_min_m && N >= 1 && K >= kStepK
+                             ? wo_prefill_workspace_bytes(M, N, K, weight_bits, kWoCounterBytes) : 0;
+  if (M > 64) return std::max(kWoCounterBytes, prefill);
   const size_t stream = wo_stream_workspace_bytes(M, N, K, weight_bits);
-  if (weight_bits != 4 || M < 1 || M > 64 || N < 1 || K < kStepK) return stream;
-  return std::max(stream, kWoCounterBytes + wo_panel_partial_bytes(M, N, K));
+  if (weight_bits != 4 || M < 1 || N < 1 || K < kStepK) return std::max(stream, prefill);
+  return std::max({stream, prefill, kWoCounterBytes + wo_panel_partial_bytes(M, N, K)});
 }
 
 extern "C" int miq_w8a16_gemm(const void* x, int64_t ldx, const int8_t* q, const void* scale,

@@ -29,6 +29,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "miq_common.h"
 #include "wo_core.h"
 
 namespace miq {
@@ -381,8 +382,10 @@ PrefillPlan plan_prefill(int kind, int64_t M, int64_t N, int64_t K) {
   const int64_t tiles = ((M + kPM - 1) / kPM) * ((N + kPN - 1) / kPN);
   PrefillPlan pl{1, steps, 0};
   constexpr int64_t kSlots = 2 * 256;  // resident workgroups (2 per CU, 256 CUs)
-  if (tiles >= kSlots / 2) return pl;
+  const int forced = tuning().wo_prefill_s;  // MIQ_WO_PREFILL_S, for tuning runs
+  if (tiles >= kSlots / 2 && forced <= 0) return pl;
   int S = (int)std::min<int64_t>((kSlots + tiles - 1) / tiles, std::max(1, steps / 8));
+  if (forced > 0) S = std::min(forced, steps);
   S = std::min(S, 16);
   if (S <= 1) return pl;
   int per = (steps + S - 1) / S;

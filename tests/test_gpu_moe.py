@@ -213,3 +213,39 @@ def test_quant_experts_int8_takes_the_fused_path():
     fused = qe(hd, idd, wd)
     grouped = qe._grouped(hd, idd, wd)
     assert rel_error(fused, grouped) < 1e-2
+
+
+@pytest.mark.parametrize("kind,k,tiled", [("int4", 8, False), ("int4", 8, True), ("int4", 12, False),
+                                          ("int8", 8, False)])
+def test_fused_moe_padding_expert_id(kind, k, tiled, miq_env):
+    """Slots routed to expert id E (the reference loop's padding class, one_hot with E + 1
+    classes, modules.py:55-75) contribute nothing; the other slots of the same token are
+    still added in ascending expert order. k = 12 takes the combine's 16-slot variant."""
+    from kernels.fused_moe import fused_moe_int4, fused_moe_int8
+    if tiled:
+        miq_env("MIQ_MOE_TILED", "1")
+    case(f"fused {kind} moe with padding ids k={k} tiled={tiled}")
+    T, H, I, E = 40, 512, 256, 16
+    g = torch.Generator().manual_seed(17)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
+    wdn = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)
+    hidden, w, idx = routed(T, H, E, k, seed=18)
+    idx = idx.clone()
+    idx[::3, 0] = E       # one padding slot in every third token
+    idx[1::7, :] = E      # tokens with every slot padded: output zero
+    if kind == "int4":
+        gu, dn = O.int4_quantize(wgu, 128), O.int4_quantize(wdn, 128)
+        loop = MO.quant_experts_loop(hidden, O.int4_linear, gu, dn, idx, w, E).float()
+        got = fused_moe_int4(hidden.to(DEV), idx.to(DEV), w.to(DEV), gu["qweight"].to(DEV), gu["scale"].to(DEV),
+                             gu["zero"].to(DEV), dn["qweight"].to(DEV), dn["scale"].to(DEV), dn["zero"].to(DEV))
+    else:
+        gu, dn = O.int8_quantize(wgu), O.int8_quantize(wdn)
+        loop = MO.quant_experts_loop(hidden, O.int8_linear, gu, dn, idx, w, E).float()
+        got = fused_moe_int8(hidden.to(DEV), idx.to(DEV), w.to(DEV), gu["qweight"].to(DEV), gu["scale"].to(DEV),
+                             dn["qweight"].to(DEV), dn["scale"].to(DEV))
+    got = got.float().cpu()
+    assert (got[1::7] == 0).all()
+    err = (got - loop).abs()
+    print(f"[bound] {kind} moe padding ids: max |fused - reference loop| {err.max().item():.4f}", flush=True)
+    assert rel_error(got, loop) < 2e-2
+    assert (err <= 2e-2 + 3e-2 * loop.abs()).all(), err.max().item()
