@@ -367,7 +367,15 @@ constexpr int kMoeChunk = 16;  // k-steps of activations staged at once
 #endif
 constexpr int kItemsPerRun = MIQ_MOE_RUN;  // consecutive items per workgroup (one staging)
 
-template <int KIND, int MODE, bool HZ, int SD, bool G1>
+// SL (16-bit scales, at most kMoeLdsGroups groups per row, a multiple of 4): at the start
+// of an item each lane loads the scale and zero words of its row's groups 4 g .. 4 g + 3
+// with one 8-byte load each, and the wavefront keeps them in its LDS slice [tile][group]
+// [row] as (scale | zero << 16); a k-step then reads one LDS word per tile instead of
+// issuing two 4-byte global loads.
+constexpr int kMoeLdsGroups = 16;
+constexpr size_t kMoeScaleLds = (size_t)4 * 2 * kMoeLdsGroups * kTile * 4;  // 4 wavefronts, 2 tiles
+
+template <int KIND, int MODE, bool HZ, int SD, bool G1, bool SL = false>
 __global__ void __launch_bounds__(256)
 moe_stream_kernel(MoeParams p, int blocks_per_tile) {
   extern __shared__ __align__(16) uint16_t lds[];
@@ -388,6 +396,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
   const int npad = *p.num_padded;
   const int xstride = kMoeChunk * kStepK + 8;
   float* xsum = reinterpret_cast<float*>(lds + kTile * xstride);
+  uint32_t* scz = reinterpret_cast<uint32_t*>(xsum + kMoeChunk * kTile) + wv * (2 * kMoeLdsGroups * kTile);
   const int wbytes = (int)((int64_t)p.E * rows_per_expert * ldw);
   constexpr int esz = SD == MIQ_F32 ? 4 : 2;
   const int sbytes = (int)(((int64_t)p.E * rows_per_expert * ngroups * esz + 3) & ~3LL);
@@ -464,23 +473,49 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
             wq[d + h][t][0] = *reinterpret_cast<const uint4*>(&v);
           }
         }
-#ifdef MIQ_MOE_ABL_NOSCALE
-        sq[d][t] = 0x3c003c00u; zq[d][t] = 0u; (void)keep;
-#else
+        if (SL) continue;  // the item's scales are in LDS
         const int gi = soff[t] + kl / p.group_steps;  // (int4 only past here)
         const int so = ((gi * esz) & ~3 & keep) | (kOut & ~keep);
         sq[d][t] = __builtin_amdgcn_raw_buffer_load_b32(srs, so, 0, 0);
         zq[d][t] = HZ ? __builtin_amdgcn_raw_buffer_load_b32(zrs, so, 0, 0) : 0u;
-#endif
       }
     };
     if (stage && tid < kTile) {
       const int pair = p.sorted_ids[tile * kTile + tid];
       s_src[tid] = pair < p.num_pairs ? (MODE == MOE_GU ? pair / p.topk : tile * kTile + tid) : -1;
     }
+    // SL: this lane's 4 groups of each tile (loads past the row's groups return zeros)
+    uint32_t scw[NR][2], zcw[NR][2];
+    if constexpr (SL) {
+#pragma unroll
+      for (int t = 0; t < NR; ++t) {
+        const int so = 4 * g < (int)ngroups ? (int)((soff[t] + 4 * g) * 2) : kOut;
+        const auto vs = __builtin_amdgcn_raw_buffer_load_b64(srs, so, 0, 0);
+        scw[t][0] = vs[0];
+        scw[t][1] = vs[1];
+        if (HZ) {
+          const auto vz = __builtin_amdgcn_raw_buffer_load_b64(zrs, so, 0, 0);
+          zcw[t][0] = vz[0];
+          zcw[t][1] = vz[1];
+        } else {
+          zcw[t][0] = zcw[t][1] = 0u;
+        }
+      }
+    }
 #pragma unroll
     for (int d = 0; d < D; ++d) request(d, d);
     __syncthreads();  // s_src ready (and the previous item is done with LDS)
+    if constexpr (SL) {
+      // (only this wavefront reads its slice, in program order after these writes)
+#pragma unroll
+      for (int t = 0; t < NR; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t sw = scw[t][j >> 1], zw = zcw[t][j >> 1];
+          const uint32_t sh = (j & 1) ? sw >> 16 : sw & 0xffffu, zh = (j & 1) ? zw >> 16 : zw & 0xffffu;
+          if (4 * g + j < (int)ngroups) scz[(t * kMoeLdsGroups + 4 * g + j) * kTile + r] = sh | (zh << 16);
+        }
+    }
 
     uint4 wnext[NR];
     // Per quantization group, T = sum_k x (128 + u) + kXBias * sum_k x (MFMA chains and the
@@ -566,7 +601,9 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
               if (G1) {
                 // one-step groups: chains from the step's bias and from zero; the group ends here
                 const int gi = soff[t] + c_grp;
-                const float sc = word_to_f32<SD>(sq[d][t], gi);
+                uint32_t scw_l = 0;
+                if constexpr (SL) scw_l = scz[(t * kMoeLdsGroups + c_grp) * kTile + r];
+                const float sc = SL ? sd_to_f32<SD>(scw_l & 0xffffu) : word_to_f32<SD>(sq[d][t], gi);
                 f32x4 c0v = mfma(av[0], bv[0], xb);
                 f32x4 c1v = mfma(av[1], bv[1], z4);
                 c0v = mfma(av[2], bv[2], c0v);
@@ -574,7 +611,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(sc, c0v[v] + c1v[v], acc[t][v]);
                 if (HZ) {
-                  const float zs = word_to_f32<SD>(zq[d][t], gi) * (1.f / kXBias);
+                  const float zs = (SL ? sd_to_f32<SD>(scw_l >> 16) : word_to_f32<SD>(zq[d][t], gi)) * (1.f / kXBias);
 #pragma unroll
                   for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(zs, xb[v], acc[t][v]);
                 }
@@ -589,11 +626,13 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
 #pragma unroll
               for (int t = 0; t < NR; ++t) {
                 const int gi = soff[t] + c_grp;
-                const float sc = word_to_f32<SD>(sq[d][t], gi);
+                uint32_t scw_l = 0;
+                if constexpr (SL) scw_l = scz[(t * kMoeLdsGroups + c_grp) * kTile + r];
+                const float sc = SL ? sd_to_f32<SD>(scw_l & 0xffffu) : word_to_f32<SD>(sq[d][t], gi);
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(sc, accg[t][v] + xsg[v], acc[t][v]);
                 if (HZ) {
-                  const float zs = word_to_f32<SD>(zq[d][t], gi) * (1.f / kXBias);
+                  const float zs = (SL ? sd_to_f32<SD>(scw_l >> 16) : word_to_f32<SD>(zq[d][t], gi)) * (1.f / kXBias);
 #pragma unroll
                   for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(zs, xsg[v], acc[t][v]);
                 }
@@ -646,24 +685,37 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
   }
 }
 
+template <int KIND, int MODE, bool HZ, int SD, bool G1, bool SL>
+void launch_stream_mode(const MoeParams& p, int grid, size_t lds, int blocks, hipStream_t st) {
+  static std::once_flag lds_once;  // the LDS limit is set once per kernel (thread-safe)
+  std::call_once(lds_once, [] {
+    allow_max_dynamic_lds(reinterpret_cast<const void*>(&moe_stream_kernel<KIND, MODE, HZ, SD, G1, SL>));
+  });
+  hipLaunchKernelGGL((moe_stream_kernel<KIND, MODE, HZ, SD, G1, SL>), dim3(grid), dim3(256), lds + (SL ? kMoeScaleLds : 0),
+                     st, p, blocks);
+}
+
 template <int KIND, bool HZ, int SD, bool G1>
 void launch_stream_experts_g(const MoeParams& p, int max_tiles, hipStream_t st) {
-  const int steps_gu = p.H / kStepK, steps_dn = p.I / kStepK;
-  const size_t lds_gu = (size_t)kTile * (kMoeChunk * kStepK + 8) * 2 + (size_t)kMoeChunk * kTile * 4;
+  const size_t lds = (size_t)kTile * (kMoeChunk * kStepK + 8) * 2 + (size_t)kMoeChunk * kTile * 4;
   const int bgu = p.I / 64, bdn = p.H / 128;
-  (void)steps_gu;
-  (void)steps_dn;
-  // the LDS limit is set once per kernel (thread-safe)
-  static std::once_flag lds_once;
-  std::call_once(lds_once, [&] {
-    allow_max_dynamic_lds(reinterpret_cast<const void*>(&moe_stream_kernel<KIND, MOE_GU, HZ, SD, G1>));
-    allow_max_dynamic_lds(reinterpret_cast<const void*>(&moe_stream_kernel<KIND, MOE_DN, HZ, SD, G1>));
-  });
   // about two workgroups per CU, never more than the runs of items that could exist
   const int grid_gu = std::max(1, std::min(512, max_tiles * bgu / kItemsPerRun));
   const int grid_dn = std::max(1, std::min(512, max_tiles * bdn / kItemsPerRun));
-  hipLaunchKernelGGL((moe_stream_kernel<KIND, MOE_GU, HZ, SD, G1>), dim3(grid_gu), dim3(256), lds_gu, st, p, bgu);
-  hipLaunchKernelGGL((moe_stream_kernel<KIND, MOE_DN, HZ, SD, G1>), dim3(grid_dn), dim3(256), lds_gu, st, p, bdn);
+  // int4 with 16-bit scales: per-item scales in LDS where a row's groups fit
+  auto lds_scales = [&](int K) {
+    const int ng = K / kStepK / p.group_steps;
+    return KIND == KIND_INT4 && SD != MIQ_F32 && ng % 4 == 0 && ng <= kMoeLdsGroups;
+  };
+  if constexpr (KIND == KIND_INT4 && SD != MIQ_F32) {
+    if (lds_scales(p.H)) launch_stream_mode<KIND, MOE_GU, HZ, SD, G1, true>(p, grid_gu, lds, bgu, st);
+    else launch_stream_mode<KIND, MOE_GU, HZ, SD, G1, false>(p, grid_gu, lds, bgu, st);
+    if (lds_scales(p.I)) launch_stream_mode<KIND, MOE_DN, HZ, SD, G1, true>(p, grid_dn, lds, bdn, st);
+    else launch_stream_mode<KIND, MOE_DN, HZ, SD, G1, false>(p, grid_dn, lds, bdn, st);
+  } else {
+    launch_stream_mode<KIND, MOE_GU, HZ, SD, G1, false>(p, grid_gu, lds, bgu, st);
+    launch_stream_mode<KIND, MOE_DN, HZ, SD, G1, false>(p, grid_dn, lds, bdn, st);
+  }
 }
 
 // one-step (128-code) groups have their own instantiation

@@ -48,17 +48,21 @@ def routed(T, H, E, k, seed):
     return hidden, w.to(torch.bfloat16), idx
 
 
-@pytest.mark.parametrize("T,H,I,E,k,sym", [(64, 2048, 1024, 64, 8, False), (64, 2048, 1024, 64, 8, True),
-                                             (1, 2048, 1024, 64, 8, False), (5, 256, 128, 8, 2, False),
-                                             (33, 512, 256, 6, 3, True)])
-def test_fused_int4_moe_matches_reference(T, H, I, E, k, sym):
+@pytest.mark.parametrize("T,H,I,E,k,sym,group", [(64, 2048, 1024, 64, 8, False, 128), (64, 2048, 1024, 64, 8, True, 128),
+                                                   (1, 2048, 1024, 64, 8, False, 128), (5, 256, 128, 8, 2, False, 128),
+                                                   (33, 512, 256, 6, 3, True, 128), (40, 2048, 1024, 16, 4, False, 256),
+                                                   (24, 4096, 512, 8, 2, True, 128), (24, 1024, 512, 8, 2, False, 512)])
+def test_fused_int4_moe_matches_reference(T, H, I, E, k, sym, group):
+    """Scales of the streaming kernels come from LDS where a row has 4, 8, 12 or 16 groups
+    (the first six shapes' gate/up; H = 4096 with 32 groups, 2-group rows and group 512
+    take the per-step scale loads)."""
     from kernels.fused_moe import fused_moe_int4
-    case(f"fused int4 moe T={T} H={H} I={I} E={E} k={k} sym={sym}")
+    case(f"fused int4 moe T={T} H={H} I={I} E={E} k={k} sym={sym} group={group}")
     g = torch.Generator().manual_seed(7)
     wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
     wdn = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)
     qf = O.int4_quantize_symmetric if sym else O.int4_quantize
-    gu, dn = qf(wgu, 128), qf(wdn, 128)
+    gu, dn = qf(wgu, group), qf(wdn, group)
     hidden, w, idx = routed(T, H, E, k, seed=8)
     want = MO.int4_experts_reference(hidden, gu, dn, w, idx)
     got = fused_moe_int4(hidden.to(DEV), idx.to(DEV), w.to(DEV), gu["qweight"].to(DEV), gu["scale"].to(DEV),
