@@ -38,6 +38,10 @@ Tuning read_tuning() {
   const char* fw = getenv("MIQ_FP8_WAVES");
   t.fp8_four_waves = fw && atoi(fw) == 4;
   t.moe_tiled = flag("MIQ_MOE_TILED");
+  const char* mw = getenv("MIQ_MOE_WAVES");
+  t.moe_four_waves = mw && atoi(mw) == 4;
+  const char* ml = getenv("MIQ_MOE_LDS_SCALES");
+  t.moe_no_lds_scales = ml && atoi(ml) == 0;
   t.moe_align_scan = flag("MIQ_MOE_ALIGN_SCAN");
   return t;
 }

@@ -188,6 +188,8 @@ struct Tuning {
   bool fp8_old;               // MIQ_FP8_OLD: the previous FP8 GEMM kernel family
   bool fp8_four_waves;        // MIQ_FP8_WAVES=4
   bool moe_tiled;             // MIQ_MOE_TILED: the tiled expert kernels
+  bool moe_four_waves;        // MIQ_MOE_WAVES=4: four-wavefront streaming expert workgroups
+  bool moe_no_lds_scales;     // MIQ_MOE_LDS_SCALES=0: per-k-step scale loads instead of LDS
   bool moe_align_scan;        // MIQ_MOE_ALIGN_SCAN: the one-wavefront-per-expert align
 };
 const Tuning& tuning();

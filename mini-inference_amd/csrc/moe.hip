@@ -18,6 +18,8 @@
 
 #include <mutex>
 
+#include <type_traits>
+
 #include "wo_core.h"
 
 namespace miq {
@@ -360,7 +362,10 @@ enum { MOE_GU = 0, MOE_DN = 1 };
 // ring depth in k-steps: one pair of k-steps per weight tile in flight. On MI355X at the
 // OLMoE layer the layer took 69.5-70.3 us with 2, 70.3-71.1 with 4, 74-75 with 6 and
 // 77-78 with 8 (16 slower still): fewer loads in flight per wavefront is faster here
-constexpr int kMoeD = 2;
+#ifndef MIQ_MOE_D
+#define MIQ_MOE_D 2
+#endif
+constexpr int kMoeD = MIQ_MOE_D;
 constexpr int kMoeChunk = 16;  // k-steps of activations staged at once
 #ifndef MIQ_MOE_RUN
 #define MIQ_MOE_RUN 2
@@ -373,11 +378,13 @@ constexpr int kItemsPerRun = MIQ_MOE_RUN;  // consecutive items per workgroup (o
 // [row] as (scale | zero << 16); a k-step then reads one LDS word per tile instead of
 // issuing two 4-byte global loads.
 constexpr int kMoeLdsGroups = 16;
-constexpr size_t kMoeScaleLds = (size_t)4 * 2 * kMoeLdsGroups * kTile * 4;  // 4 wavefronts, 2 tiles
+template <bool HZ>
+constexpr size_t kMoeScaleLdsPerWave = (size_t)2 * kMoeLdsGroups * kTile * (HZ ? 4 : 2);  // 2 tiles
 
-template <int KIND, int MODE, bool HZ, int SD, bool G1, bool SL = false>
-__global__ void __launch_bounds__(256)
+template <int KIND, int MODE, bool HZ, int SD, bool G1, bool SL, int NW>
+__global__ void __launch_bounds__(NW * 64)
 moe_stream_kernel(MoeParams p, int blocks_per_tile) {
+  constexpr int kThreads = NW * 64;
   extern __shared__ __align__(16) uint16_t lds[];
   __shared__ int s_src[kTile];
   // int8 experts: a k-step of a tile is two 128-byte line loads (rows 0-7 and 8-15), the
@@ -396,7 +403,9 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
   const int npad = *p.num_padded;
   const int xstride = kMoeChunk * kStepK + 8;
   float* xsum = reinterpret_cast<float*>(lds + kTile * xstride);
-  uint32_t* scz = reinterpret_cast<uint32_t*>(xsum + kMoeChunk * kTile) + wv * (2 * kMoeLdsGroups * kTile);
+  // SL slice of this wavefront: (scale | zero << 16) words, or 16-bit scales without zero points
+  using ScEntry = std::conditional_t<HZ, uint32_t, uint16_t>;
+  ScEntry* scz = reinterpret_cast<ScEntry*>(xsum + kMoeChunk * kTile) + wv * (2 * kMoeLdsGroups * kTile);
   const int wbytes = (int)((int64_t)p.E * rows_per_expert * ldw);
   constexpr int esz = SD == MIQ_F32 ? 4 : 2;
   const int sbytes = (int)(((int64_t)p.E * rows_per_expert * ngroups * esz + 3) & ~3LL);
@@ -416,7 +425,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
   const bool one_chunk = steps <= kMoeChunk;
   int staged_tile = -1;
   if (MODE == MOE_GU)  // every pair starts unranked (-1); the down kernel ranks the routed ones
-    for (int i = blockIdx.x * 256 + tid; i < p.num_pairs; i += gridDim.x * 256) p.rank[i] = -1;
+    for (int i = blockIdx.x * kThreads + tid; i < p.num_pairs; i += gridDim.x * kThreads) p.rank[i] = -1;
   for (int k = 0;; ++k) {
     const int item = (blockIdx.x + (k / kItemsPerRun) * gridDim.x) * kItemsPerRun + k % kItemsPerRun;
     const int tile = item / blocks_per_tile, blk = item - tile * blocks_per_tile;
@@ -427,11 +436,11 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
     // weight rows of this wavefront's two tiles (within the whole [E * rows] matrix)
     int row[NR];
     if (MODE == MOE_GU) {
-      const int c0 = blk * 64 + wv * 16;
+      const int c0 = blk * (16 * NW) + wv * 16;
       row[0] = e * rows_per_expert + c0 + r;
       row[1] = e * rows_per_expert + p.I + c0 + r;
     } else {
-      const int n0 = blk * 128 + wv * 32;
+      const int n0 = blk * (32 * NW) + wv * 32;
       row[0] = e * rows_per_expert + n0 + r;
       row[1] = e * rows_per_expert + n0 + 16 + r;
     }
@@ -513,7 +522,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
         for (int j = 0; j < 4; ++j) {
           const uint32_t sw = scw[t][j >> 1], zw = zcw[t][j >> 1];
           const uint32_t sh = (j & 1) ? sw >> 16 : sw & 0xffffu, zh = (j & 1) ? zw >> 16 : zw & 0xffffu;
-          if (4 * g + j < (int)ngroups) scz[(t * kMoeLdsGroups + 4 * g + j) * kTile + r] = sh | (zh << 16);
+          if (4 * g + j < (int)ngroups) scz[(t * kMoeLdsGroups + 4 * g + j) * kTile + r] = (ScEntry)(sh | (zh << 16));
         }
     }
 
@@ -534,11 +543,11 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
       const int xcols = nst * (kStepK / 8);
       const int npieces = kTile * xcols;
       if (c0) __syncthreads();
-      for (int base = 0; base < (stage ? npieces : 0); base += 4 * 256) {
+      for (int base = 0; base < (stage ? npieces : 0); base += 4 * kThreads) {
         uint4 xr[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int i = min(base + tid + j * 256, npieces - 1);
+          const int i = min(base + tid + j * kThreads, npieces - 1);
           const int m = i / xcols, c = i - m * xcols;
           const int src = s_src[m];
           xr[j] = src >= 0 ? *reinterpret_cast<const uint4*>(xbase + (int64_t)src * ldx + (int64_t)c0 * kStepK + c * 8)
@@ -546,7 +555,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int i = base + tid + j * 256;
+          const int i = base + tid + j * kThreads;
           const int ic = min(i, npieces - 1);
           const int m = ic / xcols, c = ic - m * xcols;
           *reinterpret_cast<uint4*>(lds + m * xstride + c * 8) = I8 ? xr[j] : permute_for_u4(xr[j]);
@@ -659,7 +668,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
     }
     // epilogue: lane (r, g) holds rows m = 4 g + v of columns r of both tiles
     if (MODE == MOE_GU) {
-      const int col = blk * 64 + wv * 16 + r;
+      const int col = blk * (16 * NW) + wv * 16 + r;
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int m = g * 4 + v;
@@ -675,7 +684,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
         const int pair = p.sorted_ids[tile * kTile + m];
         if (pair < p.num_pairs) {
           const float w = load_scalar(p.topk_w, p.w_dtype, pair);
-          const int n0 = blk * 128 + wv * 32 + r;
+          const int n0 = blk * (32 * NW) + wv * 32 + r;
           if (blk == 0 && wv == 0 && r == 0) p.rank[pair] = tile * kTile + m;
           p.ypair[(int64_t)pair * p.H + n0] = f32_to_bf16(bf16r(bf16r(acc[0][v]) * w));
           p.ypair[(int64_t)pair * p.H + n0 + 16] = f32_to_bf16(bf16r(bf16r(acc[1][v]) * w));
@@ -685,37 +694,51 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
   }
 }
 
-template <int KIND, int MODE, bool HZ, int SD, bool G1, bool SL>
+template <int KIND, int MODE, bool HZ, int SD, bool G1, bool SL, int NW>
 void launch_stream_mode(const MoeParams& p, int grid, size_t lds, int blocks, hipStream_t st) {
   static std::once_flag lds_once;  // the LDS limit is set once per kernel (thread-safe)
   std::call_once(lds_once, [] {
-    allow_max_dynamic_lds(reinterpret_cast<const void*>(&moe_stream_kernel<KIND, MODE, HZ, SD, G1, SL>));
+    allow_max_dynamic_lds(reinterpret_cast<const void*>(&moe_stream_kernel<KIND, MODE, HZ, SD, G1, SL, NW>));
   });
-  hipLaunchKernelGGL((moe_stream_kernel<KIND, MODE, HZ, SD, G1, SL>), dim3(grid), dim3(256), lds + (SL ? kMoeScaleLds : 0),
-                     st, p, blocks);
+  hipLaunchKernelGGL((moe_stream_kernel<KIND, MODE, HZ, SD, G1, SL, NW>), dim3(grid), dim3(NW * 64),
+                     lds + (SL ? NW * kMoeScaleLdsPerWave<HZ> : 0), st, p, blocks);
+}
+
+// One GEMM of the layer: NW = 8 wavefronts (twice the weight rows per staged activation
+// tile, four wavefronts per SIMD) where the sizes divide and two such workgroups fit a CU's
+// LDS, else 4; int4 with 16-bit scales keeps the item's scales in LDS where a row's groups
+// fit. MIQ_MOE_WAVES=4 forces four wavefronts.
+template <int KIND, int MODE, bool HZ, int SD, bool G1>
+void launch_stream_gemm(const MoeParams& p, int max_tiles, hipStream_t st) {
+  const size_t lds = (size_t)kTile * (kMoeChunk * kStepK + 8) * 2 + (size_t)kMoeChunk * kTile * 4;
+  const int K = MODE == MOE_GU ? p.H : p.I;
+  const int ng = K / kStepK / p.group_steps;
+  constexpr bool kSL16 = KIND == KIND_INT4 && SD != MIQ_F32;
+  const bool sl = kSL16 && ng % 4 == 0 && ng <= kMoeLdsGroups && !tuning().moe_no_lds_scales;
+  const int per8 = MODE == MOE_GU ? 16 * 8 : 32 * 8;  // weight columns / rows of an 8-wavefront item
+  const int nout = MODE == MOE_GU ? p.I : p.H;
+  const bool w8 = !tuning().moe_four_waves && nout % per8 == 0 &&
+                  2 * (lds + (sl ? 8 * kMoeScaleLdsPerWave<HZ> : 0)) <= (size_t)160 * 1024;
+  const int blocks = nout / (w8 ? per8 : per8 / 2);
+  // about two workgroups per CU, never more than the runs of items that could exist
+  const int grid = std::max(1, std::min(512, max_tiles * blocks / kItemsPerRun));
+#define MIQ_MOE_GO(SL_, NW_) launch_stream_mode<KIND, MODE, HZ, SD, G1, SL_, NW_>(p, grid, lds, blocks, st)
+  if constexpr (kSL16) {
+    if (sl && w8) MIQ_MOE_GO(true, 8);
+    else if (sl) MIQ_MOE_GO(true, 4);
+    else if (w8) MIQ_MOE_GO(false, 8);
+    else MIQ_MOE_GO(false, 4);
+  } else {
+    if (w8) MIQ_MOE_GO(false, 8);
+    else MIQ_MOE_GO(false, 4);
+  }
+#undef MIQ_MOE_GO
 }
 
 template <int KIND, bool HZ, int SD, bool G1>
 void launch_stream_experts_g(const MoeParams& p, int max_tiles, hipStream_t st) {
-  const size_t lds = (size_t)kTile * (kMoeChunk * kStepK + 8) * 2 + (size_t)kMoeChunk * kTile * 4;
-  const int bgu = p.I / 64, bdn = p.H / 128;
-  // about two workgroups per CU, never more than the runs of items that could exist
-  const int grid_gu = std::max(1, std::min(512, max_tiles * bgu / kItemsPerRun));
-  const int grid_dn = std::max(1, std::min(512, max_tiles * bdn / kItemsPerRun));
-  // int4 with 16-bit scales: per-item scales in LDS where a row's groups fit
-  auto lds_scales = [&](int K) {
-    const int ng = K / kStepK / p.group_steps;
-    return KIND == KIND_INT4 && SD != MIQ_F32 && ng % 4 == 0 && ng <= kMoeLdsGroups;
-  };
-  if constexpr (KIND == KIND_INT4 && SD != MIQ_F32) {
-    if (lds_scales(p.H)) launch_stream_mode<KIND, MOE_GU, HZ, SD, G1, true>(p, grid_gu, lds, bgu, st);
-    else launch_stream_mode<KIND, MOE_GU, HZ, SD, G1, false>(p, grid_gu, lds, bgu, st);
-    if (lds_scales(p.I)) launch_stream_mode<KIND, MOE_DN, HZ, SD, G1, true>(p, grid_dn, lds, bdn, st);
-    else launch_stream_mode<KIND, MOE_DN, HZ, SD, G1, false>(p, grid_dn, lds, bdn, st);
-  } else {
-    launch_stream_mode<KIND, MOE_GU, HZ, SD, G1, false>(p, grid_gu, lds, bgu, st);
-    launch_stream_mode<KIND, MOE_DN, HZ, SD, G1, false>(p, grid_dn, lds, bdn, st);
-  }
+  launch_stream_gemm<KIND, MOE_GU, HZ, SD, G1>(p, max_tiles, st);
+  launch_stream_gemm<KIND, MOE_DN, HZ, SD, G1>(p, max_tiles, st);
 }
 
 // one-step (128-code) groups have their own instantiation

@@ -253,3 +253,33 @@ def test_fused_moe_padding_expert_id(kind, k, tiled, miq_env):
     print(f"[bound] {kind} moe padding ids: max |fused - reference loop| {err.max().item():.4f}", flush=True)
     assert rel_error(got, loop) < 2e-2
     assert (err <= 2e-2 + 3e-2 * loop.abs()).all(), err.max().item()
+
+
+@pytest.mark.parametrize("T,H,I,E,k,sym,env", [(64, 2048, 1024, 64, 8, True, "MIQ_MOE_WAVES"),
+                                               (33, 512, 256, 6, 3, False, "MIQ_MOE_WAVES"),
+                                               (64, 2048, 1024, 64, 8, False, "MIQ_MOE_LDS_SCALES"),
+                                               (24, 384, 256, 8, 2, True, None)])
+def test_fused_int4_moe_streaming_variants(T, H, I, E, k, sym, env, miq_env):
+    """The streaming expert kernels' other layouts: four wavefronts per workgroup
+    (MIQ_MOE_WAVES=4; also taken without the switch by the down GEMM when H is not a
+    multiple of 256, as in the last shape, H = 384) and per-k-step scale loads
+    (MIQ_MOE_LDS_SCALES=0)."""
+    from kernels.fused_moe import fused_moe_int4
+    if env == "MIQ_MOE_WAVES":
+        miq_env(env, "4")
+    elif env:
+        miq_env(env, "0")
+    case(f"fused int4 moe variant {env} T={T} H={H} I={I} E={E} k={k} sym={sym}")
+    g = torch.Generator().manual_seed(19)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
+    wdn = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)
+    qf = O.int4_quantize_symmetric if sym else O.int4_quantize
+    gu, dn = qf(wgu, 128), qf(wdn, 128)
+    hidden, w, idx = routed(T, H, E, k, seed=20)
+    want = MO.int4_experts_reference(hidden, gu, dn, w, idx)
+    got = fused_moe_int4(hidden.to(DEV), idx.to(DEV), w.to(DEV), gu["qweight"].to(DEV), gu["scale"].to(DEV),
+                         None if sym else gu["zero"].to(DEV), dn["qweight"].to(DEV), dn["scale"].to(DEV),
+                         None if sym else dn["zero"].to(DEV))
+    assert rel_error(got, want) < 2e-2
+    err = (got.float().cpu() - want).abs()
+    assert (err <= 1e-2 + 2e-2 * want.abs()).all(), err.max().item()
