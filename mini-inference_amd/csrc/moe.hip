@@ -360,17 +360,11 @@ moe_down_kernel(MoeParams p, int chunk_steps) {
 //                 times the routing weight goes to ypair[pair]
 enum { MOE_GU = 0, MOE_DN = 1 };
 // ring depth in k-steps: one pair of k-steps per weight tile in flight. On MI355X at the
-// OLMoE layer the layer took 69.5-70.3 us with 2, 70.3-71.1 with 4, 74-75 with 6 and
-// 77-78 with 8 (16 slower still): fewer loads in flight per wavefront is faster here
-#ifndef MIQ_MOE_D
-#define MIQ_MOE_D 2
-#endif
-constexpr int kMoeD = MIQ_MOE_D;
+// OLMoE layer (four-wavefront workgroups, per-step scale loads) the layer took 69.5-70.3
+// us with 2, 70.3-71.1 with 4, 74-75 with 6 and 77-78 with 8 (16 slower still); with
+// eight-wavefront workgroups and LDS scales 4 measured the same as 2
+constexpr int kMoeD = 2;
 constexpr int kMoeChunk = 16;  // k-steps of activations staged at once
-#ifndef MIQ_MOE_RUN
-#define MIQ_MOE_RUN 2
-#endif
-constexpr int kItemsPerRun = MIQ_MOE_RUN;  // consecutive items per workgroup (one staging)
 
 // SL (16-bit scales, at most kMoeLdsGroups groups per row, a multiple of 4): at the start
 // of an item each lane loads the scale and zero words of its row's groups 4 g .. 4 g + 3
@@ -383,7 +377,7 @@ constexpr size_t kMoeScaleLdsPerWave = (size_t)2 * kMoeLdsGroups * kTile * (HZ ?
 
 template <int KIND, int MODE, bool HZ, int SD, bool G1, bool SL, int NW>
 __global__ void __launch_bounds__(NW * 64)
-moe_stream_kernel(MoeParams p, int blocks_per_tile) {
+moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
   constexpr int kThreads = NW * 64;
   extern __shared__ __align__(16) uint16_t lds[];
   __shared__ int s_src[kTile];
@@ -420,14 +414,14 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
   int nsteps_v = steps;
   asm volatile("" : "+v"(nsteps_v));
 
-  // a workgroup takes runs of kItemsPerRun consecutive items: they share a tile, so when
-  // the whole K fits one chunk its activations are staged once per run
+  // a workgroup takes runs of `run` consecutive items: they share a tile, so when the
+  // whole K fits one chunk its activations are staged once per run
   const bool one_chunk = steps <= kMoeChunk;
   int staged_tile = -1;
   if (MODE == MOE_GU)  // every pair starts unranked (-1); the down kernel ranks the routed ones
     for (int i = blockIdx.x * kThreads + tid; i < p.num_pairs; i += gridDim.x * kThreads) p.rank[i] = -1;
   for (int k = 0;; ++k) {
-    const int item = (blockIdx.x + (k / kItemsPerRun) * gridDim.x) * kItemsPerRun + k % kItemsPerRun;
+    const int item = (blockIdx.x + (k / run) * gridDim.x) * run + k % run;
     const int tile = item / blocks_per_tile, blk = item - tile * blocks_per_tile;
     if (tile * kTile >= npad) break;
     const bool stage = !(one_chunk && tile == staged_tile);
@@ -695,13 +689,13 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile) {
 }
 
 template <int KIND, int MODE, bool HZ, int SD, bool G1, bool SL, int NW>
-void launch_stream_mode(const MoeParams& p, int grid, size_t lds, int blocks, hipStream_t st) {
+void launch_stream_mode(const MoeParams& p, int grid, size_t lds, int blocks, int run, hipStream_t st) {
   static std::once_flag lds_once;  // the LDS limit is set once per kernel (thread-safe)
   std::call_once(lds_once, [] {
     allow_max_dynamic_lds(reinterpret_cast<const void*>(&moe_stream_kernel<KIND, MODE, HZ, SD, G1, SL, NW>));
   });
   hipLaunchKernelGGL((moe_stream_kernel<KIND, MODE, HZ, SD, G1, SL, NW>), dim3(grid), dim3(NW * 64),
-                     lds + (SL ? NW * kMoeScaleLdsPerWave<HZ> : 0), st, p, blocks);
+                     lds + (SL ? NW * kMoeScaleLdsPerWave<HZ> : 0), st, p, blocks, run);
 }
 
 // One GEMM of the layer: NW = 8 wavefronts (twice the weight rows per staged activation
@@ -721,8 +715,14 @@ void launch_stream_gemm(const MoeParams& p, int max_tiles, hipStream_t st) {
                   2 * (lds + (sl ? 8 * kMoeScaleLdsPerWave<HZ> : 0)) <= (size_t)160 * 1024;
   const int blocks = nout / (w8 ? per8 : per8 / 2);
   // about two workgroups per CU, never more than the runs of items that could exist
-  const int grid = std::max(1, std::min(512, max_tiles * blocks / kItemsPerRun));
-#define MIQ_MOE_GO(SL_, NW_) launch_stream_mode<KIND, MODE, HZ, SD, G1, SL_, NW_>(p, grid, lds, blocks, st)
+  // runs of two items per workgroup where there are enough items for two workgroups per CU
+  // even so (OLMoE layer, MI355X: with eight-wavefront workgroups and 512 items per GEMM,
+  // runs of 1 took 56.2 us, of 2 61.5 us; with four wavefronts and 1024 items, runs of 2
+  // measured 70 us against 77-84 for 1, 3 or 4)
+  const int items = max_tiles * blocks;
+  const int run = items >= 2 * 512 ? 2 : 1;
+  const int grid = std::max(1, std::min(512, items / run));
+#define MIQ_MOE_GO(SL_, NW_) launch_stream_mode<KIND, MODE, HZ, SD, G1, SL_, NW_>(p, grid, lds, blocks, run, st)
   if constexpr (kSL16) {
     if (sl && w8) MIQ_MOE_GO(true, 8);
     else if (sl) MIQ_MOE_GO(true, 4);
