@@ -3,10 +3,11 @@
 //   y[m, n] = sum_k x[m, k] * W[n, k],  x bf16 [M, K],  W int8 [N, K] or int4 [N, K/2]
 //
 // Work decomposition:
-//   * a workgroup of 4 wavefronts owns a row block of 4 * NR tiles of 16 weight rows and
-//     a K range (one of S splits along grid.y); wavefront w owns tiles w * NR .. + NR - 1
-//     over the whole range, so the activations it multiplies are shared by the 4
-//     wavefronts through LDS (x is read from L2 once per row block, not once per tile);
+//   * a workgroup of W wavefronts (4 for one activation tile, 8 for several) owns a row
+//     block of W * NR tiles of 16 weight rows and a K range (one of S splits along
+//     grid.y); wavefront w owns tiles w * NR .. + NR - 1 over the whole range, so the
+//     activations it multiplies are shared by the W wavefronts through LDS (x is read
+//     from L2 once per row block, not once per tile);
 //   * the activations of a chunk of the range are staged in LDS by a short loop; while a
 //     thread writes its pieces it also adds their 8 values, and a 16-lane DPP reduction
 //     gives sum_k x over every k-step, which removes the +128 code offset (below) with 4
@@ -60,9 +61,12 @@ namespace {
 
 using namespace wo;
 
-// wavefronts per workgroup (8 and 16 for decode tiles measured slower than 4)
+// wavefronts per workgroup: 4 for one activation tile (8 and 16 measured slower); 8 for
+// several (one weight tile each: twice the wavefronts per SIMD over the same staged
+// activations; int8 gate/up on MI355X, M = 32 / 64: 20.4 / 30.5 against 21.6 / 33.5 us
+// with 4 wavefronts of two tiles)
 template <int MT>
-constexpr int waves_for() { return 4; }
+constexpr int waves_for() { return MT >= 2 ? 8 : 4; }
 constexpr int kMaxCounters = 4096;   // row blocks that may use split-K
 constexpr int kCounterBytes = kMaxCounters * 4;
 
@@ -555,9 +559,9 @@ StreamPlan plan_stream(int kind, int64_t M, int64_t N, int64_t K, int group_step
   pl.units = (int)(steps / pl.unit_steps);
   pl.MT = (int)((M + 15) / 16);
   pl.mtiles = 1;
-  // two weight tiles per wavefront (x reused twice from LDS) when there are many rows;
-  // with few rows one tile, which keeps the partials a row block reads back small
-  pl.NR = pl.MT >= 2 && N > 8192 ? 2 : 1;
+  // one weight tile per wavefront: several activation tiles take eight-wavefront
+  // workgroups (a row block of 128 rows, as two tiles per wavefront of four did)
+  pl.NR = 1;
   int S = 0;
   // M split: one activation tile of 16 rows per workgroup and two weight tiles per
   // wavefront. The workgroups of one row block on its different activation tiles share
