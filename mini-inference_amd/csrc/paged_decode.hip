@@ -92,6 +92,13 @@ __device__ inline void bytes8_to_bf16(uint32_t w0, uint32_t w1, uint32_t out[4])
   }
 }
 
+// 16-byte streaming load (each K / V byte is read once): non-temporal
+__device__ inline uint4 load_nt16(const uint8_t* p) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 __device__ inline f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
@@ -528,7 +535,7 @@ paged_decode_split8_kernel(AttnParams p) {
       for (int c = 0; c < 2; ++c) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
-          kr[bi][s][c][h] = *reinterpret_cast<const uint4*>(p.k + (int64_t)kls[s][c][h] * p.kvs_t + head_off + kchunk);
+          kr[bi][s][c][h] = load_nt16(p.k + (int64_t)kls[s][c][h] * p.kvs_t + head_off + kchunk);
         if (HAS_SCALE) ksr[bi][s][c] = load_sd_raw<SD>(p.ks, (int64_t)ks[s][c] * p.ss_t + (int64_t)kvh * p.ss_h);
       }
   };
@@ -537,7 +544,7 @@ paged_decode_split8_kernel(AttnParams p) {
 #pragma unroll
     for (int s = 0; s < CS; ++s) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vr[bi][s][i] = *reinterpret_cast<const uint4*>(p.v + (int64_t)vs[s][i] * p.kvs_t + head_off + dseg);
+      for (int i = 0; i < 4; ++i) vr[bi][s][i] = load_nt16(p.v + (int64_t)vs[s][i] * p.kvs_t + head_off + dseg);
       if (HAS_SCALE) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) vsr[bi][s][c] = load_sd_raw<SD>(p.vs, (int64_t)ks[s][c] * p.ss_t + (int64_t)kvh * p.ss_h);
