@@ -82,10 +82,9 @@ using namespace miq;
 extern "C" size_t miq_wo_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits) {
   const size_t prefill = M >= tuning().wo_prefill_min_m && N >= 1 && K >= kStepK
                              ? wo_prefill_workspace_bytes(M, N, K, weight_bits, kWoCounterBytes) : 0;
-  if (M > 64) return std::max(kWoCounterBytes, prefill);
   const size_t stream = wo_stream_workspace_bytes(M, N, K, weight_bits);
-  if (weight_bits != 4 || M < 1 || N < 1 || K < kStepK) return std::max(stream, prefill);
-  return std::max({stream, prefill, kWoCounterBytes + wo_panel_partial_bytes(M, N, K)});
+  if (weight_bits != 4 || M < 1 || N < 1 || K < kStepK) return std::max({kWoCounterBytes, stream, prefill});
+  return std::max({kWoCounterBytes, stream, prefill, kWoCounterBytes + wo_panel_partial_bytes(M, N, K)});
 }
 
 extern "C" int miq_w8a16_gemm(const void* x, int64_t ldx, const int8_t* q, const void* scale,
