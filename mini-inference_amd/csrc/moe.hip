@@ -768,12 +768,17 @@ __global__ void moe_combine_kernel(const uint16_t* __restrict__ ypair, const int
   int rk[KT];
   uint2 v[KT];
   int nvalid = 0;  // slots routed to an expert (rank >= 0; an out-of-range id keeps -1)
+  // the value loads do not wait for the ranks: a slot's row is read whatever its rank (an
+  // unranked slot's row is inside the buffer and its value is not used)
 #pragma unroll
   for (int i = 0; i < KT; ++i) {
-    const int r = i < topk ? rank[(int64_t)t * topk + i] : -1;
-    rk[i] = r >= 0 ? r : 0x7fffffff;
-    nvalid += r >= 0 ? 1 : 0;
-    v[i] = r >= 0 ? *reinterpret_cast<const uint2*>(row + (int64_t)i * H) : make_uint2(0, 0);
+    rk[i] = i < topk ? rank[(int64_t)t * topk + i] : -1;
+    v[i] = i < topk ? *reinterpret_cast<const uint2*>(row + (int64_t)i * H) : make_uint2(0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < KT; ++i) {
+    nvalid += rk[i] >= 0 ? 1 : 0;
+    rk[i] = rk[i] >= 0 ? rk[i] : 0x7fffffff;
   }
   int pos[KT];
 #pragma unroll
