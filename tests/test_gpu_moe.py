@@ -283,3 +283,31 @@ def test_fused_int4_moe_streaming_variants(T, H, I, E, k, sym, env, miq_env):
     assert rel_error(got, want) < 2e-2
     err = (got.float().cpu() - want).abs()
     assert (err <= 1e-2 + 2e-2 * want.abs()).all(), err.max().item()
+
+
+@pytest.mark.parametrize("kind,sdt", [("int4", torch.float32), ("int4", torch.float16), ("int8", torch.float32),
+                                      ("int8", torch.float16)])
+def test_fused_moe_scale_dtypes(kind, sdt):
+    """Scales (and zero points) in fp32 (INT4: the per-k-step scale loads; 16-bit scales take
+    the LDS slots) and fp16, against the same references as the bf16 tests."""
+    from kernels.fused_moe import fused_moe_int4, fused_moe_int8
+    case(f"fused {kind} moe with {sdt} scales")
+    T, H, I, E, k = 24, 1024, 512, 8, 2
+    g = torch.Generator().manual_seed(21)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
+    wdn = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)
+    hidden, w, idx = routed(T, H, E, k, seed=22)
+    if kind == "int4":
+        gu, dn = O.int4_quantize(wgu, 128, sdt), O.int4_quantize(wdn, 128, sdt)
+        want = MO.int4_experts_reference(hidden, gu, dn, w, idx)
+        got = fused_moe_int4(hidden.to(DEV), idx.to(DEV), w.to(DEV), gu["qweight"].to(DEV), gu["scale"].to(DEV),
+                             gu["zero"].to(DEV), dn["qweight"].to(DEV), dn["scale"].to(DEV), dn["zero"].to(DEV))
+        err = (got.float().cpu() - want).abs()
+        assert (err <= 1e-2 + 2e-2 * want.abs()).all(), err.max().item()
+    else:
+        gu, dn = O.int8_quantize(wgu, sdt), O.int8_quantize(wdn, sdt)
+        loop = MO.quant_experts_loop(hidden, O.int8_linear, gu, dn, idx, w, E).float()
+        got = fused_moe_int8(hidden.to(DEV), idx.to(DEV), w.to(DEV), gu["qweight"].to(DEV), gu["scale"].to(DEV),
+                             dn["qweight"].to(DEV), dn["scale"].to(DEV)).float().cpu()
+        err = (got - loop).abs()
+        assert (err <= 1e-2 + 2e-2 * loop.abs()).all(), err.max().item()
