@@ -388,7 +388,7 @@ paged_decode_split_kernel(AttnParams p) {
 //     transposed in registers (byte permutes) and written to LDS per 32-token step;
 //     masking of V past the context is only done in the chunk that reaches it.
 template <int KVT, bool HAS_SCALE, int SD, int CS, int NC, int W, bool P16 = false>
-__global__ void __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(W >= 8 ? 4 : 2)))
+__global__ void __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2)))
 paged_decode_split8_kernel(AttnParams p) {
   const int part = blockIdx.y, kvh = blockIdx.x, b = blockIdx.z;  // kv heads of one partition are dispatched together (they share DRAM pages)
   const int L = p.lens[b];
@@ -408,40 +408,23 @@ paged_decode_split8_kernel(AttnParams p) {
   // (8-bit codes, row-major); after the token loop the V area holds the wave's O rows
   constexpr int kPRowC = kChunk + 8;       // P row stride (bf16)
   constexpr int kVRowB = kD + 16;          // V row stride (bytes)
-  // 8-wavefront workgroups (4 per SIMD, 128 VGPRs) keep q in LDS and merge the wavefronts'
-  // O rows 4 heads at a time, so two of them fit a CU; 4-wavefront ones keep q in registers
-  // and merge all 16 rows at once (the LDS variant measured slower there)
-  constexpr bool kLean = W >= 8;
-  constexpr int kMergeRows = kLean ? 4 : 16;  // O rows merged per pass
-  constexpr int kVBytes = kChunk * kVRowB > kMergeRows * (kD + 4) * 4 ? kChunk * kVRowB : kMergeRows * (kD + 4) * 4;
+  constexpr int kVBytes = kChunk * kVRowB > 16 * (kD + 4) * 4 ? kChunk * kVRowB : 16 * (kD + 4) * 4;
   __shared__ __align__(16) uint16_t s_p[W][16 * kPRowC];
   __shared__ __align__(16) uint8_t s_v[W][kVBytes];
   __shared__ float s_m[W][16], s_l[W][16];
-  __shared__ uint4 s_qf[kLean ? 4 : 1][64];
 
-  bf16x8 qf[kLean ? 1 : 4];
+  bf16x8 qf[4];
   {
     const bool real = r < GROUP;
     // MFMA j of lane (g, r) takes dims 16 g + 8 j (j < 2) and 64 + 16 g + 8 (j - 2): the
-    // order in which the K loads below deliver a token's 128 bytes. In LDS every wavefront
-    // writes the same values and a lane reads back only the words it wrote, so no barrier
-    // is needed.
+    // order in which the K loads below deliver a token's 128 bytes
     const uint16_t* qp = p.q + (int64_t)b * p.qs_b + (int64_t)(kvh * GROUP + (real ? r : 0)) * p.qs_h + g * 16;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint4 u = real ? *reinterpret_cast<const uint4*>(qp + (j < 2 ? 8 * j : 64 + 8 * (j - 2))) : make_uint4(0, 0, 0, 0);
-      if constexpr (kLean) s_qf[j][lane] = u;
-      else qf[j] = bf16x8_from(u.x, u.y, u.z, u.w);
+      qf[j] = bf16x8_from(u.x, u.y, u.z, u.w);
     }
   }
-  auto q_frag = [&](int j) -> bf16x8 {
-    if constexpr (kLean) {
-      const uint4 u = s_qf[j][lane];
-      return bf16x8_from(u.x, u.y, u.z, u.w);
-    } else {
-      return qf[j];
-    }
-  };
   for (int i = lane; i < 16 * kPRowC; i += 64) s_p[wv][i] = 0;
 
   const int per_wave = p.partition / W;
@@ -542,11 +525,7 @@ paged_decode_split8_kernel(AttnParams p) {
       for (int i = 0; i < 4; ++i) vs[s][i] = (int)slot_of(min(c0 + s * kStep + tq + i, t_end - 1));
     }
   };
-  // register sets (chunk c + 1 loads while chunk c computes); workgroups of 8 wavefronts
-  // take one set and 4 wavefronts per SIMD instead: with two sets (160 VGPRs) only one such
-  // workgroup fits a CU (MI355X, FP8 cache, 512-token partitions: 170 against 188 us per
-  // step; with 4 wavefronts, 256-token partitions, one set measured 194 against 147 us)
-  constexpr int NB = NC > 1 && W < 8 ? 2 : 1;
+  constexpr int NB = NC > 1 ? 2 : 1;  // register sets (chunk c + 1 loads while chunk c computes)
   uint4 kr[NB][CS][2][2], vr[NB][CS][4];
   uint32_t ksr[NB][CS][2], vsr[NB][CS][2];
   auto issue_k = [&](int bi, const KSlots& ks) {
@@ -590,7 +569,7 @@ paged_decode_split8_kernel(AttnParams p) {
         bytes8_to_bf16<KVT>(k1.z, k1.w, o); kf[3] = bf16x8_from(o[0], o[1], o[2], o[3]);
         f32x4 s4 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s4 = mfma16(q_frag(j), kf[j], s4);
+        for (int j = 0; j < 4; ++j) s4 = mfma16(qf[j], kf[j], s4);
         const bool valid = c0 + s * kStep + c * 16 + r < t_end;
         const float kscale = HAS_SCALE ? qk_scale * sd_to_f32<SD>(ksr[bi][s][c]) : qk_scale;
 #pragma unroll
@@ -728,54 +707,35 @@ paged_decode_split8_kernel(AttnParams p) {
       s_l[wv][g * 4 + v] = lsum;
     }
   }
-  // the wavefronts' O rows go through each wavefront's V area, all 16 rows at once, or
-  // (8-wavefront workgroups) 4 heads at a time: the heads 4 g + v sit in row group g
   float* s_o_w = reinterpret_cast<float*>(s_v[wv]);
-  auto merge_rows = [&](int h0, int nh) {  // heads h0 .. h0 + nh - 1, at rows 0 .. nh - 1
-    for (int e2 = tid; e2 < nh * 16; e2 += W * 64) {
-      const int hl = e2 >> 4, hh = h0 + hl, dq = (e2 & 15) * 8;
-      float mx = -__builtin_inff();
-      for (int w = 0; w < W; ++w) mx = fmaxf(mx, s_m[w][hh]);
-      const float ms = mx == -__builtin_inff() ? 0.f : mx;
-      float lt = 0.f, sw[W];
-      for (int w = 0; w < W; ++w) {
-        sw[w] = exp2_le0(s_m[w][hh] - ms);
-        lt += s_l[w][hh] * sw[w];
-      }
-      const int h = kvh * GROUP + hh;
-      const int64_t base = ((int64_t)b * p.H + h) * p.max_parts + part;
-      const float inv = lt > 0.f ? 1.f / lt : 0.f;
-      float* op = p.o_part + base * kD + dq;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float o = 0.f;
-        for (int w = 0; w < W; ++w)
-          o += reinterpret_cast<const float*>(s_v[w])[hl * (kD + 4) + dq + e] * sw[w];
-        op[e] = o * inv;
-      }
-      if ((e2 & 15) == 0) p.lse_part[base] = lt > 0.f ? (mx + log2f(lt)) * kLn2 : -__builtin_inff();
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) s_o_w[(g * 4 + v) * (kD + 4) + j * 16 + r] = o_acc[j][v];
+  __syncthreads();
+
+  for (int e2 = tid; e2 < GROUP * 16; e2 += W * 64) {
+    const int hh = e2 >> 4, dq = (e2 & 15) * 8;
+    float mx = -__builtin_inff();
+    for (int w = 0; w < W; ++w) mx = fmaxf(mx, s_m[w][hh]);
+    const float ms = mx == -__builtin_inff() ? 0.f : mx;
+    float lt = 0.f, sw[W];
+    for (int w = 0; w < W; ++w) {
+      sw[w] = exp2_le0(s_m[w][hh] - ms);
+      lt += s_l[w][hh] * sw[w];
     }
-  };
-  if constexpr (!kLean) {
+    const int h = kvh * GROUP + hh;
+    const int64_t base = ((int64_t)b * p.H + h) * p.max_parts + part;
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    float* op = p.o_part + base * kD + dq;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int v = 0; v < 4; ++v) s_o_w[(g * 4 + v) * (kD + 4) + j * 16 + r] = o_acc[j][v];
-    __syncthreads();
-    merge_rows(0, GROUP);
-  } else {
-    for (int h0 = 0; h0 < GROUP; h0 += kMergeRows) {
-      if (h0) __syncthreads();  // the previous heads are merged
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int hl = g * 4 + v - h0;
-          if (hl >= 0 && hl < kMergeRows) s_o_w[hl * (kD + 4) + j * 16 + r] = o_acc[j][v];
-        }
-      __syncthreads();
-      merge_rows(h0, min(kMergeRows, GROUP - h0));
+    for (int e = 0; e < 8; ++e) {
+      float o = 0.f;
+      for (int w = 0; w < W; ++w)
+        o += reinterpret_cast<const float*>(s_v[w])[hh * (kD + 4) + dq + e] * sw[w];
+      op[e] = o * inv;
     }
+    if ((e2 & 15) == 0) p.lse_part[base] = lt > 0.f ? (mx + log2f(lt)) * kLn2 : -__builtin_inff();
   }
   MIQ_TRACE(4);
 }
@@ -838,14 +798,18 @@ void launch_split3(const AttnParams& p, dim3 grid, hipStream_t st) {
     // 4-chunk pipeline needs more than 256 VGPRs); any other partition: 4 wavefronts,
     // chunk after chunk
     // 16-token pages (the reference's block size) take the scalar page-id path, whose
-    // wavefronts each run 2 chunks of 32 tokens (2 / 4 / 8 wavefronts for 128 / 256 / 512-
-    // token partitions). At the Qwen3 decode shape on MI355X: 256 143.7 against 146.0-146.3
-    // us with 2 chunks of 64 (2 wavefronts of 4 chunks of 32 the same as 2 of 2 x 64, one
-    // chunk of 128 per wavefront 10 % slower); 512 143-144 against 150-151; 128 149-150
-    // against 151.5-152
+    // wavefronts run chunks of 32 tokens through the two register sets: 2 / 4 wavefronts of
+    // 2 chunks for 128 / 256-token partitions, 4 wavefronts of 4 and 8 chunks for 512 and
+    // 1024. At the Qwen3 decode shape on MI355X (FP8): 256 143.7 against 146.0-146.3 us with
+    // 2 chunks of 64 (2 wavefronts of 4 chunks the same, one chunk of 128 per wavefront
+    // 10 % slower); 128 149-150 against 151.5-152; 512 143 us with 4 wavefronts of 4 chunks
+    // against 159 with 8 wavefronts of 2 (a longer pipeline per wavefront, fewer workgroups);
+    // 1024 144 us
     const bool p16 = p.page == 16;
-    if (p.partition == 512 && p16)
-      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 1, 2, 8, true>), grid, dim3(8 * 64), 0, st, p);
+    if (p.partition == 1024 && p16)
+      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 1, 8, 4, true>), grid, dim3(4 * 64), 0, st, p);
+    else if (p.partition == 512 && p16)
+      hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 1, 4, 4, true>), grid, dim3(4 * 64), 0, st, p);
     else if (p.partition == 512)
       hipLaunchKernelGGL((paged_decode_split8_kernel<KVT, HS, SD, 2, 2, 4>), grid, dim3(4 * 64), 0, st, p);
     else if (p.partition == 256 && p16)

@@ -95,11 +95,11 @@ def test_partitions_agree():
 @pytest.mark.parametrize("kind", ["int8", "fp8"])
 @pytest.mark.parametrize("partition,lens", [(None, [40, 7, 90]), (128, [600, 7, 1290, 300]),
                                             (256, [600, 7, 1290, 300]), (384, [600, 7, 1290]),
-                                            (512, [600, 7, 1290, 1100])])
+                                            (512, [600, 7, 1290, 1100]), (1024, [2500, 7, 1290, 1100])])
 @pytest.mark.parametrize("H,KV", [(4, 4), (32, 2)])
 def test_quantized_cache_written_by_kvcache(kind, partition, lens, H, KV):
     """reference tests/test_paged_attention.py:73-89 with the HIP quantize-on-write; every
-    partition size with its own kernel instance (128, 256, 512) and the generic one (384),
+    partition size with its own kernel instance (128, 256, 512, 1024) and the generic one (384),
     with requests that end inside a chunk, a partition, or after one token; one kv head per
     q head, and the largest group the kernels take (16 q heads per kv head)."""
     from engine.core.kv_cache import KVCache
@@ -142,7 +142,7 @@ def test_benchmark_shape(kind):
 
 
 @pytest.mark.parametrize("kind", ["bf16", "fp8", "int8"])
-@pytest.mark.parametrize("partition", [128, 256, 512, 384])
+@pytest.mark.parametrize("partition", [128, 256, 512, 384, 1024])
 def test_max_len_below_the_longest_context(kind, partition):
     """A stale or undersized max_len never cuts a request: when a context does not fit
     max_parts partitions, its partitions grow (multiples of the partition size) so the
