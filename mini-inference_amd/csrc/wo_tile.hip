@@ -133,24 +133,10 @@ wo_tile_kernel(TileParams p) {
   // bit operations (a select would become a branch around each load)
   int nsteps_v = nst;
   asm volatile("" : "+v"(nsteps_v));
-  // int4: raw loads of k-steps d, d + 1 (d even) in wq[d], wq[d + 1]; int8: wq[d][0..1]
-  constexpr int NL = KIND == KIND_INT4 ? 1 : 2;
-  uint4 wq[NS][NL];
-#pragma unroll
-  for (int d = 0; d < NS; ++d) {
-    if (KIND == KIND_INT8 || (d & 1) == 0) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int kp = ((d + (KIND == KIND_INT4 ? lc2 : 0) - nsteps_v) >> 31) & wok[h];
-        const int off = ((woff[h] + d * kStepBytes) & kp) | (kOut & ~kp);
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2 /* nt */);
-        if (KIND == KIND_INT4) wq[d + h][0] = *reinterpret_cast<const uint4*>(&v);
-        else wq[d][h] = *reinterpret_cast<const uint4*>(&v);
-      }
-    }
-  }
   // int4: the scale (and zero) words of the slice's groups, at most NS of them, with two
-  // 16-byte loads from the aligned word holding the first one
+  // 16-byte loads from the aligned word holding the first one. They are requested before
+  // the weights: the multiply of k-step d then waits only for the weight loads up to d
+  // (loads complete in issue order), not for the last one
   constexpr int esz = SD == MIQ_F32 ? 4 : 2;
   uint32_t sw[8], zw[8];
   const int sbase = r < nrows ? (soff * esz) & ~3 : kOut - 32;
@@ -164,6 +150,22 @@ wo_tile_kernel(TileParams p) {
         const auto vz = __builtin_amdgcn_raw_buffer_load_b128(zrs, sbase + 16 * h, 0, 0);
         const uint4 uz = *reinterpret_cast<const uint4*>(&vz);
         zw[4 * h] = uz.x; zw[4 * h + 1] = uz.y; zw[4 * h + 2] = uz.z; zw[4 * h + 3] = uz.w;
+      }
+    }
+  }
+  // int4: raw loads of k-steps d, d + 1 (d even) in wq[d], wq[d + 1]; int8: wq[d][0..1]
+  constexpr int NL = KIND == KIND_INT4 ? 1 : 2;
+  uint4 wq[NS][NL];
+#pragma unroll
+  for (int d = 0; d < NS; ++d) {
+    if (KIND == KIND_INT8 || (d & 1) == 0) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int kp = ((d + (KIND == KIND_INT4 ? lc2 : 0) - nsteps_v) >> 31) & wok[h];
+        const int off = ((woff[h] + d * kStepBytes) & kp) | (kOut & ~kp);
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2 /* nt */);
+        if (KIND == KIND_INT4) wq[d + h][0] = *reinterpret_cast<const uint4*>(&v);
+        else wq[d][h] = *reinterpret_cast<const uint4*>(&v);
       }
     }
   }
