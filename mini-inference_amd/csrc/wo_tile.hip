@@ -133,6 +133,10 @@ wo_tile_kernel(TileParams p) {
   // bit operations (a select would become a branch around each load)
   int nsteps_v = nst;
   asm volatile("" : "+v"(nsteps_v));
+  // int8: the row scale of the output this thread writes at the end (thread t < 16 M
+  // writes row n0 + t % 16), requested now rather than after the reduction
+  uint32_t row_scale = 0;
+  if (KIND == KIND_INT8 && tid < M * 16) row_scale = load_sd_raw<SD>(p.scale, min(n0 + (tid & 15), p.N - 1));
   // int4: the scale (and zero) words of the slice's groups, at most NS of them, with two
   // 16-byte loads from the aligned word holding the first one. They are requested before
   // the weights: the multiply of k-step d then waits only for the weight loads up to d
@@ -305,6 +309,7 @@ wo_tile_kernel(TileParams p) {
     if (m < M) red[(wv * M + m) * 16 + r] = acc[v];
   }
   __syncthreads();
+  // kThreads >= 256 >= 16 M: one output per thread at most
   for (int t = tid; t < M * 16; t += kThreads) {
     const int m = t >> 4, n = n0 + (t & 15);
     if ((t & 15) >= nrows) continue;
@@ -312,7 +317,7 @@ wo_tile_kernel(TileParams p) {
 #pragma unroll
     for (int w = 0; w < W; ++w) o += red[w * M * 16 + t];
     if (KIND == KIND_INT8)
-      o = bf16_to_f32(f32_to_bf16(o)) * bf16_to_f32(f32_to_bf16(sd_to_f32<SD>(load_sd_raw<SD>(p.scale, n))));
+      o = bf16_to_f32(f32_to_bf16(o)) * bf16_to_f32(f32_to_bf16(sd_to_f32<SD>(row_scale)));
     p.y[(int64_t)m * p.ldy + n] = f32_to_bf16(o);
   }
   MIQ_TRACE(4);
