@@ -21,13 +21,15 @@
 //     acc += s_g * (sum x (128 + u) + bias * sum x) [+ z_g * sum x], with the scale (and
 //     zero) of that step's group, so any group size multiple of 128 works; int8: the sums
 //     over all K, then y = bf16(bf16(acc - 128 sum x) * bf16(s)) as int8_wo.linear.
-// A launch with fewer tiles than CUs splits K; the last workgroup of a tile to arrive adds
-// the fp32 partials in split order and leaves the workspace zero again.
+// A launch may split K (plan_prefill: so that the items fill whole rounds of resident
+// workgroups); the last workgroup of a tile to arrive adds the fp32 partials in split
+// order and leaves the workspace zero again.
 // Tiles are handed to XCDs in contiguous blocks (consecutive workgroup ids go to different
 // XCDs), so an XCD's L2 keeps the weight panels of its block while the activations come
 // from the MALL.
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 #include "miq_common.h"
 #include "wo_core.h"
@@ -373,28 +375,57 @@ struct PrefillPlan {
   size_t partial_bytes;  // S > 1: [S][M][N] fp32
 };
 
-// A launch with fewer tiles than CUs splits K (whole 128-byte weight units, at least 8
-// k-steps per split) into about two workgroups per CU. (At 304 tiles of a 19456 x 2560
-// weight a split of 2 measured slower: the partial round trip costs more than it returns.)
-PrefillPlan plan_prefill(int kind, int64_t M, int64_t N, int64_t K) {
+// K splits (whole 128-byte weight units) are chosen by a cost model of the launch. 512
+// workgroups are resident at once (2 per CU, 256 CUs), so `tiles * S` items take
+// ceil(tiles * S / 512) rounds of steps / S k-steps each; every split adds an fp32 partial
+// tile that is stored, counted and read back by the last arriver. On MI355X (INT4 and
+// INT8, N x K = 2560 x 9728 and 19456 x 2560, M = 256 ... 2048) the launch time followed
+//   rounds * steps * 1.45 us / S  +  (S > 1) * S * M * N * 4 bytes / (1 TB/s)
+// to about 10 %: e.g. 2560 x 9728 at M = 512 (160 tiles) took 85 us with S = 4 (640 items,
+// two rounds) and 54.5 us with S = 3 (480 items, one round). The S of least modelled time
+// is taken (the smaller on ties), with splits of at least 4 k-steps, at most 16 splits,
+// partials within kPrefillMaxPartials (so that the no-allocation entry point, whose
+// scratch holds that much, plans the same splits) and one counter per tile.
+constexpr size_t kPrefillMaxPartials = (size_t)30 << 20;
+PrefillPlan plan_prefill(int kind, int64_t M, int64_t N, int64_t K, size_t counter_bytes) {
   const int spu = kind == KIND_INT4 ? 2 : 1;
   const int steps = (int)(K / kStepK);
   const int64_t tiles = ((M + kPM - 1) / kPM) * ((N + kPN - 1) / kPN);
   PrefillPlan pl{1, steps, 0};
   constexpr int64_t kSlots = 2 * 256;  // resident workgroups (2 per CU, 256 CUs)
+  constexpr double kStepUs = 1.45, kPartialBytesPerUs = 1e6;
+  auto partial_bytes = [&](int S) { return (size_t)S * (size_t)M * (size_t)N * 4; };
+  // splits of `per` k-steps (rounded to whole units); returns the split count
+  auto splits_for = [&](int S) {
+    int per = (steps + S - 1) / S;
+    per = (per + spu - 1) / spu * spu;
+    return std::pair<int, int>((steps + per - 1) / per, per);
+  };
+  const bool counters_ok = tiles * 4 <= (int64_t)counter_bytes;
   const int forced = tuning().wo_prefill_s;  // MIQ_WO_PREFILL_S, for tuning runs
-  if (tiles >= kSlots / 2 && forced <= 0) return pl;
-  int S = (int)std::min<int64_t>((kSlots + tiles - 1) / tiles, std::max(1, steps / 8));
-  if (forced > 0) S = std::min(forced, steps);
-  S = std::min(S, 16);
-  if (S <= 1) return pl;
-  int per = (steps + S - 1) / S;
-  per = (per + spu - 1) / spu * spu;
-  S = (steps + per - 1) / per;
-  if (S <= 1) return pl;
-  pl.S = S;
-  pl.split_steps = per;
-  pl.partial_bytes = (size_t)S * (size_t)M * (size_t)N * 4;
+  int best_s = 1, best_per = steps;
+  if (forced > 0) {
+    const auto sp = splits_for(std::min(forced, steps));
+    best_s = sp.first;
+    best_per = sp.second;
+  } else if (counters_ok) {
+    double best = (double)((tiles + kSlots - 1) / kSlots) * steps * kStepUs;
+    for (int S = 2; S <= 16; ++S) {
+      const auto sp = splits_for(S);
+      if (sp.first != S || sp.second < 4 || partial_bytes(S) > kPrefillMaxPartials) continue;
+      const double cost = (double)((tiles * S + kSlots - 1) / kSlots) * steps * kStepUs / S +
+                          (double)partial_bytes(S) / kPartialBytesPerUs;
+      if (cost < best) {
+        best = cost;
+        best_s = S;
+        best_per = sp.second;
+      }
+    }
+  }
+  if (best_s <= 1) return pl;
+  pl.S = best_s;
+  pl.split_steps = best_per;
+  pl.partial_bytes = partial_bytes(best_s);
   return pl;
 }
 
@@ -402,7 +433,7 @@ PrefillPlan plan_prefill(int kind, int64_t M, int64_t N, int64_t K) {
 
 // Workspace bytes of a prefill call: the counter area, then the split-K partials.
 size_t wo_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits, size_t counter_bytes) {
-  const PrefillPlan pl = plan_prefill(weight_bits == 4 ? KIND_INT4 : KIND_INT8, M, N, K);
+  const PrefillPlan pl = plan_prefill(weight_bits == 4 ? KIND_INT4 : KIND_INT8, M, N, K, counter_bytes);
   return pl.S > 1 ? counter_bytes + pl.partial_bytes : 0;
 }
 
@@ -415,7 +446,7 @@ int wo_prefill_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w
                       const char* name) {
   MIQ_REQUIRE((int64_t)N * ldw < 0x7fff0000LL, "%s: weights of %lld bytes exceed 2 GiB", name, (long long)N * ldw);
   MIQ_REQUIRE(M * ldx < (1LL << 31), "%s: activations of %lld elements exceed 2^31", name, (long long)(M * ldx));
-  const PrefillPlan pl = plan_prefill(kind, M, N, K);
+  const PrefillPlan pl = plan_prefill(kind, M, N, K, counter_bytes);
   PrefillParams p{};
   p.x = x;
   p.ldx = ldx;

@@ -13,8 +13,8 @@ from kernels import _lib as L
 SKINNY_MAX_M = 64  # decode kernels up to 64 activation rows; above, the prefill kernel
 # Largest M for which the fused prefill kernel is used by the quantization methods; above it
 # the methods dequantize and call the device GEMM, which measured faster on MI355X from
-# about these sizes (INT4: M = 1536 at 2560 x 9728 and 19456 x 2560; INT8: M = 768).
-PREFILL_MAX_M = {4: 1024, 8: 512}
+# about these sizes (INT4: M = 1536 at 19456 x 2560; INT8: M = 1024 at 2560 x 9728).
+PREFILL_MAX_M = {4: 1024, 8: 768}
 
 
 def _rows(t):
