@@ -10,13 +10,16 @@
 // MFMAs and no weight is unpacked twice in a workgroup. (128 activation rows spill at the
 // 256 registers two wavefronts per SIMD leave.)
 //   * activations: one k-step (128 k) of the 64 rows at a time goes global -> registers ->
-//     LDS (int4: in the nibble-unpack order), double buffered; the next step's loads are in
-//     flight while the current step is multiplied. While a thread writes its pieces it adds
+//     LDS (int4: in the nibble-unpack order), double buffered; int4 requests step s + 1 and
+//     int8 step s + 2 (two register sets) while step s is multiplied. While a thread writes
+//     its pieces it adds
 //     them, and a 16-lane DPP reduction gives each row's sum over the step, which removes the
 //     +128 code offset;
 //   * weights: a unit of 128 bytes per row (two int4 k-steps, one int8 k-step) is loaded as
 //     two 16-byte loads per lane and tile in address order (whole 128-byte lines), one unit
-//     ahead in a second register set; lanes_to_mfma turns them into the MFMA B layout;
+//     ahead (int4) or four (int8) in further register sets; lanes_to_mfma turns them into the
+//     MFMA B layout (on MI355X the deeper int8 pipeline took 4-9 % off the 2560 x 9728 shape;
+//     for int4 it measured 3-5 % slower at 19456 x 2560);
 //   * math: v_mfma_f32_16x16x32_bf16 on bf16 128 + code. int4: per k-step
 //     acc += s_g * (sum x (128 + u) + bias * sum x) [+ z_g * sum x], with the scale (and
 //     zero) of that step's group, so any group size multiple of 128 works; int8: the sums
@@ -62,6 +65,15 @@ struct PrefillParams {
   int* counters;        // S > 1: one arrival counter per tile, zero between calls
 };
 
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order
+template <int N, int I = 0, class F>
+__device__ inline void unroll_n(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    unroll_n<N, I + 1>(f);
+  }
+}
+
 template <int KIND, bool HZ, int SD>
 __global__ void __launch_bounds__(256, 2)
 wo_prefill_kernel(PrefillParams p) {
@@ -90,17 +102,21 @@ wo_prefill_kernel(PrefillParams p) {
   int xoff[kPieces];  // element offsets of the thread's pieces (rows past M re-read row M - 1)
 #pragma unroll
   for (int j = 0; j < kPieces; ++j) xoff[j] = min(m0 + ((tid + 256 * j) >> 4), p.M - 1) * (int)p.ldx + (tid & 15) * 8;
-  uint4 xr[kPieces];
-  auto stage_load = [&](int s) {
+  // two register sets: the pieces of step s + 2 are requested while step s is multiplied
+  uint4 xr[2][kPieces];
+  auto stage_load = [&](auto xi_c, int s) {
+    constexpr int xi = decltype(xi_c)::value;
 #pragma unroll
-    for (int j = 0; j < kPieces; ++j) xr[j] = *reinterpret_cast<const uint4*>(p.x + xoff[j] + (int64_t)(sb + s) * kStepK);
+    for (int j = 0; j < kPieces; ++j)
+      xr[xi][j] = *reinterpret_cast<const uint4*>(p.x + xoff[j] + (int64_t)(sb + s) * kStepK);
   };
-  auto stage_store = [&](int buf) {
+  auto stage_store = [&](auto xi_c, int buf) {
+    constexpr int xi = decltype(xi_c)::value;
 #pragma unroll
     for (int j = 0; j < kPieces; ++j) {
       const int row = (tid + 256 * j) >> 4;
-      *reinterpret_cast<uint4*>(&s_x[buf][row * kPRow + (tid & 15) * 8]) = I4 ? permute_for_u4(xr[j]) : xr[j];
-      float sm = sum8_bf16(xr[j]);
+      *reinterpret_cast<uint4*>(&s_x[buf][row * kPRow + (tid & 15) * 8]) = I4 ? permute_for_u4(xr[xi][j]) : xr[xi][j];
+      float sm = sum8_bf16(xr[xi][j]);
       sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x111, 0xf, 0xf, true));
       sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x112, 0xf, 0xf, true));
       sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x114, 0xf, 0xf, true));
@@ -125,13 +141,15 @@ wo_prefill_kernel(PrefillParams p) {
       wbase[t][h] = row < p.N ? row * (int)p.ldw + sb / SPU * 128 + lc2 * 64 + lcl * 16 : -1;
     }
   const int units = (ns + SPU - 1) / SPU;
-  uint4 wb[2][NT][2];
+  // weight units in flight: unit u + WR is requested once unit u has been multiplied
+  constexpr int WR = I4 ? 2 : 4;  // INT4: the loop below keeps one unit ahead
+  uint4 wb[WR][NT][2];
   // int4: the raw scale / zero words of the unit's k-steps (group of each step)
   const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.scale), 0, p.sbytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t zrs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(HZ ? p.zero : p.scale), 0, p.sbytes, 0x00020000);
   constexpr int esz = SD == MIQ_F32 ? 4 : 2;
-  uint32_t sq[2][SPU][NT], zq[2][SPU][NT];
+  uint32_t sq[WR][SPU][NT], zq[WR][SPU][NT];
   int srow[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) srow[t] = min(n0 + t * 16 + r, p.N - 1);
@@ -219,37 +237,74 @@ wo_prefill_kernel(PrefillParams p) {
     }
   };
 
-  // ---- prologue: step 0 staged, units 0 (and 1) requested
-  stage_load(0);
-  load_unit(std::integral_constant<int, 0>{}, 0);
-  stage_store(0);
-  __syncthreads();
-  // ---- main loop: two units per trip (register sets 0 and 1); step s uses LDS buffer s & 1
-  for (int u = 0; u < units; u += 2) {
-    load_unit(std::integral_constant<int, 1>{}, u + 1);
+  if constexpr (I4) {
+    // INT4 (measured faster this way on MI355X than the deeper pipeline below): step s + 1
+    // is requested while step s is multiplied and staged right after it; unit u + 1 is
+    // requested when unit u starts
+    constexpr auto X0 = std::integral_constant<int, 0>{};
+    stage_load(X0, 0);
+    load_unit(std::integral_constant<int, 0>{}, 0);
+    stage_store(X0, 0);
+    __syncthreads();
+    for (int u = 0; u < units; u += 2) {
+      load_unit(std::integral_constant<int, 1>{}, u + 1);
 #pragma unroll
-    for (int k = 0; k < SPU; ++k) {
-      const int s = u * SPU + k;
-      if (s < ns) {
-        if (s + 1 < ns) stage_load(s + 1);
-        if (k == 0) compute_step(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, s & 1, s);
-        else compute_step(std::integral_constant<int, 0>{}, std::integral_constant<int, SPU - 1>{}, s & 1, s);
-        if (s + 1 < ns) stage_store((s + 1) & 1);
-        __syncthreads();
+      for (int k = 0; k < SPU; ++k) {
+        const int s = u * SPU + k;
+        if (s < ns) {
+          if (s + 1 < ns) stage_load(X0, s + 1);
+          if (k == 0) compute_step(std::integral_constant<int, 0>{}, std::integral_constant<int, 0>{}, s & 1, s);
+          else compute_step(std::integral_constant<int, 0>{}, std::integral_constant<int, SPU - 1>{}, s & 1, s);
+          if (s + 1 < ns) stage_store(X0, (s + 1) & 1);
+          __syncthreads();
+        }
+      }
+      if (u + 1 >= units) break;
+      load_unit(std::integral_constant<int, 0>{}, u + 2);
+#pragma unroll
+      for (int k = 0; k < SPU; ++k) {
+        const int s = (u + 1) * SPU + k;
+        if (s < ns) {
+          if (s + 1 < ns) stage_load(X0, s + 1);
+          if (k == 0) compute_step(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{}, s & 1, s);
+          else compute_step(std::integral_constant<int, 1>{}, std::integral_constant<int, SPU - 1>{}, s & 1, s);
+          if (s + 1 < ns) stage_store(X0, (s + 1) & 1);
+          __syncthreads();
+        }
       }
     }
-    if (u + 1 >= units) break;
-    load_unit(std::integral_constant<int, 0>{}, u + 2);
+  } else {
+  // ---- prologue: units 0 .. WR - 1 and steps 0, 1 requested, step 0 staged
 #pragma unroll
-    for (int k = 0; k < SPU; ++k) {
-      const int s = (u + 1) * SPU + k;
-      if (s < ns) {
-        if (s + 1 < ns) stage_load(s + 1);
-        if (k == 0) compute_step(std::integral_constant<int, 1>{}, std::integral_constant<int, 0>{}, s & 1, s);
-        else compute_step(std::integral_constant<int, 1>{}, std::integral_constant<int, SPU - 1>{}, s & 1, s);
-        if (s + 1 < ns) stage_store((s + 1) & 1);
-        __syncthreads();
-      }
+    for (int w = 0; w < WR; ++w) {
+      if (w == 0) load_unit(std::integral_constant<int, 0>{}, 0);
+      else if (w == 1) load_unit(std::integral_constant<int, 1 % WR>{}, 1);
+      else if (w == 2) load_unit(std::integral_constant<int, 2 % WR>{}, 2);
+      else load_unit(std::integral_constant<int, 3 % WR>{}, 3);
+    }
+    stage_load(std::integral_constant<int, 0>{}, 0);
+    if (ns > 1) stage_load(std::integral_constant<int, 1>{}, 1);
+    stage_store(std::integral_constant<int, 0>{}, 0);
+    __syncthreads();
+    // ---- main loop: WR units (an even number of steps) per trip, so every register set and
+    // LDS buffer index is a compile-time constant. Step s multiplies LDS buffer s & 1,
+    // requests step s + 2 into the register set step s came from, stages step s + 1
+    // (requested two steps ago) into the other buffer, and after a unit's last step requests
+    // unit u + WR into that unit's registers.
+    constexpr int kBody = WR * SPU;
+    static_assert(kBody % 2 == 0, "steps per trip must be even");
+    for (int s0 = 0; s0 < ns; s0 += kBody) {
+      unroll_n<kBody>([&](auto i_c) {
+        constexpr int i = decltype(i_c)::value, bi = i / SPU, k = i % SPU;
+        const int s = s0 + i;
+        if (s < ns) {
+          if (s + 2 < ns) stage_load(std::integral_constant<int, i & 1>{}, s + 2);
+          compute_step(std::integral_constant<int, bi>{}, std::integral_constant<int, k>{}, i & 1, s);
+          if (s + 1 < ns) stage_store(std::integral_constant<int, (i + 1) & 1>{}, (i + 1) & 1);
+          __syncthreads();
+          if (k == SPU - 1) load_unit(std::integral_constant<int, bi>{}, (s0 + i) / SPU + WR);
+        }
+      });
     }
   }
 
