@@ -369,9 +369,10 @@ static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_s
   TilePlan pl{0, 0, 0, 0, 0};
   if (M < 1 || M > 16 || N < 1 || K < kStepK) return pl;
   if (tuning().wo_stream) return pl;  // force the streamed kernel (tuning, tests)
-  // int8 with more than 2 rows: the streamed kernel measured faster on MI355X (the staged
-  // activations of a tile outweigh the saved round trips there)
-  if (kind == KIND_INT8 && M > 2) return pl;
+  // int8 with more than 4 rows: the streamed kernel (N = 19456, K = 2560 on MI355X: tile
+  // kernel at M = 3 / 4 / 8 / 16 12.0 / 12.9 / 15.3 / 16.9 us, streamed 14.1 / 14.2 / 15.2 /
+  // 17.0 us; the staged activations of a tile grow with M)
+  if (kind == KIND_INT8 && M > 4) return pl;
   const int64_t steps = K / kStepK;
   int us = kind == KIND_INT4 ? group_steps : 1;
   // int4 slices start on an even k-step when they can (whole 128-byte lines per load)

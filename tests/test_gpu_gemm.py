@@ -176,7 +176,8 @@ def test_w4a16_tile_and_stream(kernel, M, N, K, group, sdt, symmetric, miq_env):
 
 
 @pytest.mark.parametrize("kernel", list(KERNELS))
-@pytest.mark.parametrize("M,N,K", [(1, 19456, 2560), (2, 4096, 2560), (3, 160, 1152), (4, 64, 9728), (1, 2512, 2560)])
+@pytest.mark.parametrize("M,N,K", [(1, 19456, 2560), (2, 4096, 2560), (3, 160, 1152), (4, 64, 9728), (1, 2512, 2560),
+                                   (8, 19456, 2560), (16, 1008, 2560), (13, 2512, 1152)])
 def test_w8a16_tile_and_stream(kernel, M, N, K, miq_env):
     from kernels import quant_ops as ops
     case(f"w8a16 {kernel} M={M} N={N} K={K}")
