@@ -791,14 +791,15 @@ __global__ void moe_combine_kernel(const uint16_t* __restrict__ ypair, const int
   float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int q = 0; q < KT; ++q) {
-    if (q >= nvalid) break;
-    uint2 w = make_uint2(0, 0);
+    if (q < nvalid) {  // rank positions past the routed slots add nothing
+      uint2 w = make_uint2(0, 0);
 #pragma unroll
-    for (int i = 0; i < KT; ++i) w = pos[i] == q ? v[i] : w;
-    s.x = bf16r(s.x + __builtin_bit_cast(float, w.x << 16));
-    s.y = bf16r(s.y + __builtin_bit_cast(float, w.x & 0xffff0000u));
-    s.z = bf16r(s.z + __builtin_bit_cast(float, w.y << 16));
-    s.w = bf16r(s.w + __builtin_bit_cast(float, w.y & 0xffff0000u));
+      for (int i = 0; i < KT; ++i) w = pos[i] == q ? v[i] : w;
+      s.x = bf16r(s.x + __builtin_bit_cast(float, w.x << 16));
+      s.y = bf16r(s.y + __builtin_bit_cast(float, w.x & 0xffff0000u));
+      s.z = bf16r(s.z + __builtin_bit_cast(float, w.y << 16));
+      s.w = bf16r(s.w + __builtin_bit_cast(float, w.y & 0xffff0000u));
+    }
   }
   const uint32_t lo = f32_to_bf16(s.x) | ((uint32_t)f32_to_bf16(s.y) << 16);
   const uint32_t hi = f32_to_bf16(s.z) | ((uint32_t)f32_to_bf16(s.w) << 16);
