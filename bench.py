@@ -341,6 +341,56 @@ def bench_moe_int8(dev):
             "experts_touched": touched, "MB_per_call": round(nbytes / 1e6, 1)}
 
 
+def bench_moe_fp8(dev):
+    """Config 5's layer with FP8 experts (e4m3fn codes, fp32 per-row scales): the fused FP8
+    path, and the grouped per-expert path it replaces (one sort, then FP8WeightAct.linear
+    per hit expert) timed eagerly beside it."""
+    from kernels import quant_ops as ops
+    from kernels.fused_moe import fused_moe_fp8
+    T, H, inter, E, k = 64, 2048, 1024, 64, 8
+    hidden, w, idx = moe_routing(T, H, E, k)
+    hidden, w, idx = hidden.to(dev), w.to(dev), idx.to(dev)
+    dg = torch.Generator(device=dev).manual_seed(9)
+    wgu = (torch.randn(E, 2 * inter, H, generator=dg, device=dev) * 0.02).to(torch.bfloat16)
+    wdn = (torch.randn(E, H, inter, generator=dg, device=dev) * 0.02).to(torch.bfloat16)
+    gu = ops.fp8_quantize_rows(wgu)
+    dn = ops.fp8_quantize_rows(wdn)
+    del wgu, wdn
+    touched = int(idx.unique().numel())
+    per_expert = 2 * inter * H + H * inter + (2 * inter + H) * 4
+    nbytes = touched * per_expert + T * H * 2 * 2 + T * k * 6
+    n = copies_for(E * per_expert, 2)
+    sets = [(gu[0].clone(), gu[1].clone(), dn[0].clone(), dn[1].clone()) for _ in range(n)]
+
+    def launch(i):
+        gq, gs, dq, ds = sets[i % len(sets)]
+        return lambda: fused_moe_fp8(hidden, idx, w, gq, gs, dq, ds)
+    reps = 8
+    t = time_graph([launch(i) for i in range(reps)]) / reps
+    gbs = nbytes / t / 1e9
+    # the grouped path (host loop with a device sync per call: timed eagerly, not in a graph)
+    from engine.quantization.fp8 import FP8WeightAct
+    from engine.quantization.modules import QuantExperts
+    method = FP8WeightAct(device=dev)
+    qe = QuantExperts.__new__(QuantExperts)
+    torch.nn.Module.__init__(qe)
+    qe.method, qe.num_experts, qe.act_fn = method, E, torch.nn.SiLU()
+    gq, gs, dq, ds = sets[0]
+    qe._store("gate_up_", {"qweight": gq, "scale": gs})
+    qe._store("down_", {"qweight": dq, "scale": ds})
+    for _ in range(2):
+        qe._grouped(hidden, idx, w)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        qe._grouped(hidden, idx, w)
+    torch.cuda.synchronize()
+    tg = (time.perf_counter() - t0) / 5
+    return {"us_per_layer": round(t * 1e6, 2), "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
+            "experts_touched": touched, "MB_per_call": round(nbytes / 1e6, 1),
+            "grouped_per_expert_path_us": round(tg * 1e6, 1)}
+
+
 # ---------------------------------------------------------------- CPU baselines (oracle)
 # The reference's CPU path restated in oracle/ (plain PyTorch), on the host cores of the
 # GPU box, at each configuration's shape; a bounded sample: whole calls until about
@@ -536,6 +586,7 @@ SECTIONS = {
     "paged_decode_int8_kv": lambda dev: bench_attention(dev, "int8"),
     "moe_int4_layer": bench_moe,
     "moe_int8_layer": bench_moe_int8,
+    "moe_fp8_layer": bench_moe_fp8,
 }
 
 

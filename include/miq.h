@@ -225,6 +225,21 @@ int miq_w8a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E
                   const int32_t* num_padded, void* workspace, size_t workspace_bytes,
                   void* out, void* stream);
 
+/* Replaces QuantExperts.forward (engine/quantization/modules.py:55-75) for FP8WeightAct
+ * experts with a SiLU gate on a native-FP8 device: the same layer as miq_w4a16_moe with
+ * every expert linear FP8WeightAct.linear (engine/quantization/fp8.py:41-61): activation
+ * rows quantized per row to e4m3fn with s = max(amax, 1e-12) / 448, then
+ * bf16(sum(x_q w_q) * s_x * s_w) as torch._scaled_mm returns it.
+ * gate_up q: e4m3fn bytes [E, 2I, H], scale fp32 [E, 2I]; down q: e4m3fn bytes [E, H, I],
+ * scale fp32 [E, H]. H and I multiples of 128 and at most 2048; sorted_ids / expert_ids /
+ * num_padded from miq_moe_align with block_m == 16; workspace from
+ * miq_moe_workspace_bytes. out: bf16 [T, H]. */
+int miq_fp8_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
+                const uint8_t* gu_q, const float* gu_scale, const uint8_t* dn_q, const float* dn_scale,
+                const void* topk_weights, int w_dtype, const int32_t* sorted_ids,
+                const int32_t* expert_ids, const int32_t* num_padded, void* workspace,
+                size_t workspace_bytes, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,7 +74,7 @@ int check_launch(const char* what) {
 
 extern "C" const char* miq_last_error(void) { return miq::g_error; }
 
-extern "C" int miq_abi_version(void) { return 2; }
+extern "C" int miq_abi_version(void) { return 3; }
 
 extern "C" int miq_tuning_reload(void) {
   std::lock_guard<std::mutex> hold(miq::g_tuning_lock);

@@ -365,6 +365,11 @@ enum { MOE_GU = 0, MOE_DN = 1 };
 // eight-wavefront workgroups and LDS scales 4 measured the same as 2
 constexpr int kMoeD = 2;
 constexpr int kMoeChunk = 16;  // k-steps of activations staged at once
+// FP8 experts (e4m3fn codes, one fp32 scale per weight row), next to wo_core's INT8 / INT4;
+// their activation rows are staged whole (K <= kMoeChunk k-steps) as e4m3 codes with a
+// per-row scale, at this LDS row pitch (16 rows read 16 bytes at one column on distinct banks)
+constexpr int KIND_FP8 = 2;
+constexpr int kF8Row = kMoeChunk * kStepK + 16;
 
 // SL (16-bit scales, at most kMoeLdsGroups groups per row, a multiple of 4): at the start
 // of an item each lane loads the scale and zero words of its row's groups 4 g .. 4 g + 3
@@ -383,20 +388,25 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
   __shared__ int s_src[kTile];
   // int8 experts: a k-step of a tile is two 128-byte line loads (rows 0-7 and 8-15), the
   // activations stay in natural order and one per-row scale is applied at the end
-  constexpr bool I8 = KIND == KIND_INT8;
-  constexpr int NR = 2, NL = I8 ? 2 : 1, D = kMoeD;
+  constexpr bool I8 = KIND == KIND_INT8, F8 = KIND == KIND_FP8;
+  constexpr bool B1 = I8 || F8;  // one byte per code: a k-step of a tile is two line loads
+  constexpr int NR = 2, NL = B1 ? 2 : 1, D = kMoeD;
+  __shared__ float s_xs[kTile];  // FP8: the activation rows' scales
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
   const int K = MODE == MOE_GU ? p.H : p.I;
   const int steps = K / kStepK;
-  const int64_t ldw = I8 ? K : K / 2;
+  const int64_t ldw = B1 ? K : K / 2;
   const int rows_per_expert = MODE == MOE_GU ? 2 * p.I : p.H;
-  const int64_t ngroups = I8 ? 1 : steps / p.group_steps;
+  const int64_t ngroups = B1 ? 1 : steps / p.group_steps;
   const uint16_t* xbase = MODE == MOE_GU ? p.hidden : p.hbuf;
   const int ldx = K;
   const int npad = *p.num_padded;
   const int xstride = kMoeChunk * kStepK + 8;
-  float* xsum = reinterpret_cast<float*>(lds + kTile * xstride);
+  // FP8 stages only the codes (kTile rows at pitch kF8Row), with the per-(row, k-step)
+  // maxima after them
+  float* xsum = F8 ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(lds) + kTile * kF8Row)
+                   : reinterpret_cast<float*>(lds + kTile * xstride);
   // SL slice of this wavefront: (scale | zero << 16) words, or 16-bit scales without zero points
   using ScEntry = std::conditional_t<HZ, uint32_t, uint16_t>;
   ScEntry* scz = reinterpret_cast<ScEntry*>(xsum + kMoeChunk * kTile) + wv * (2 * kMoeLdsGroups * kTile);
@@ -453,12 +463,12 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
     }
     uint4 wq[D][NR][NL];
     uint32_t sq[D][NR], zq[D][NR];
-    static_assert(I8 || D % 2 == 0, "int4 weight loads come in pairs of k-steps");
+    static_assert(B1 || D % 2 == 0, "int4 weight loads come in pairs of k-steps");
     auto request = [&](int d, int kl) {
       const int keep = (kl - nsteps_v) >> 31;
 #pragma unroll
       for (int t = 0; t < NR; ++t) {
-        if constexpr (I8) {
+        if constexpr (B1) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) {
             const int off = ((woff[t][h] + kl * 128) & keep) | (kOut & ~keep);
@@ -537,7 +547,78 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
       const int xcols = nst * (kStepK / 8);
       const int npieces = kTile * xcols;
       if (c0) __syncthreads();
-      for (int base = 0; base < (stage ? npieces : 0); base += 4 * kThreads) {
+      if constexpr (F8) {
+        // FP8 (the host keeps K within one chunk): the tile's activation rows are quantized
+        // as FP8WeightAct.quantize_activation does (fp8.py:41-46): per row
+        // s = max(amax |x|, 1e-12) / 448 and codes e4m3(clamp(x / s, +-448)). A first pass
+        // forms the row maxima (16 consecutive lanes hold one k-step of one row: a DPP max,
+        // then one thread per row over the k-steps); a second pass reads the pieces again
+        // (from L2) and writes the codes to LDS at row pitch kF8Row. Keeping every piece in
+        // registers between the passes cost a wavefront per SIMD.
+        if (stage) {
+          auto piece = [&](int i) -> uint4 {
+            const int m = i / xcols, c = i - m * xcols;
+            const int src = s_src[m];
+            return src >= 0 ? *reinterpret_cast<const uint4*>(xbase + (int64_t)src * ldx + c * 8) : make_uint4(0, 0, 0, 0);
+          };
+          for (int base = 0; base < npieces; base += 4 * kThreads) {
+            uint4 xr[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xr[j] = piece(min(base + tid + j * kThreads, npieces - 1));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int i = base + tid + j * kThreads;
+              const uint32_t w4[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
+              float mx = 0.f;
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                mx = fmaxf(mx, fmaxf(fabsf(bf16_to_f32(w4[q] & 0xffff)), fabsf(bf16_to_f32(w4[q] >> 16))));
+              mx = fmaxf(mx, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, mx), 0x111, 0xf, 0xf, true)));
+              mx = fmaxf(mx, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, mx), 0x112, 0xf, 0xf, true)));
+              mx = fmaxf(mx, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, mx), 0x114, 0xf, 0xf, true)));
+              mx = fmaxf(mx, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, mx), 0x118, 0xf, 0xf, true)));
+              if (i < npieces) {
+                const int m = i / xcols, c = i - m * xcols;
+                if ((c & 15) == 15) xsum[(c >> 4) * kTile + m] = mx;
+              }
+            }
+          }
+          __syncthreads();
+          if (tid < kTile) {
+            float a = 0.f;
+            for (int q = 0; q < nst; ++q) a = fmaxf(a, xsum[q * kTile + tid]);
+            s_xs[tid] = fmaxf(a, 1e-12f) / 448.0f;
+          }
+          __syncthreads();
+          uint8_t* a8 = reinterpret_cast<uint8_t*>(lds);
+          for (int base = 0; base < npieces; base += 4 * kThreads) {
+            uint4 xr[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xr[j] = piece(min(base + tid + j * kThreads, npieces - 1));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int i = base + tid + j * kThreads;
+              if (i < npieces) {
+                const int m = i / xcols, c = i - m * xcols;
+                const float sx = s_xs[m];
+                const uint32_t w4[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
+                int o[2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                  const float v0 = fminf(fmaxf(bf16_to_f32(w4[2 * h] & 0xffff) / sx, -448.f), 448.f);
+                  const float v1 = fminf(fmaxf(bf16_to_f32(w4[2 * h] >> 16) / sx, -448.f), 448.f);
+                  const float v2 = fminf(fmaxf(bf16_to_f32(w4[2 * h + 1] & 0xffff) / sx, -448.f), 448.f);
+                  const float v3 = fminf(fmaxf(bf16_to_f32(w4[2 * h + 1] >> 16) / sx, -448.f), 448.f);
+                  o[h] = __builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
+                  o[h] = __builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, o[h], true);
+                }
+                *reinterpret_cast<uint2*>(a8 + m * kF8Row + c * 8) = make_uint2((uint32_t)o[0], (uint32_t)o[1]);
+              }
+            }
+          }
+        }
+      }
+      for (int base = 0; base < (stage && !F8 ? npieces : 0); base += 4 * kThreads) {
         uint4 xr[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -566,7 +647,24 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
 #pragma unroll
         for (int d = 0; d < D; ++d) {
           const int kst = k + d, kl = kst - c0;
-          if (kst < c0 + nst) {
+          if (kst < c0 + nst && F8) {
+            // A: row r, the 16-byte chunks g and 4 + g of each 64-byte half of the k-step,
+            // the bytes lanes_to_mfma gives this lane of every weight row: both operands
+            // hold the same k positions in the same places
+            const uint8_t* a8 = reinterpret_cast<const uint8_t*>(lds) + r * kF8Row + kl * kStepK;
+            const uint4 lo = *reinterpret_cast<const uint4*>(a8 + 16 * g);
+            const uint4 hi = *reinterpret_cast<const uint4*>(a8 + 64 + 16 * g);
+            const i32x8 a8v = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+#pragma unroll
+            for (int t = 0; t < NR; ++t) {
+              uint4 wl[2];
+              lanes_to_mfma(bp_addr, wq[d][t][0], wq[d][t][1], wl[0], wl[1]);
+              const i32x8 b8v = {(int)wl[0].x, (int)wl[0].y, (int)wl[0].z, (int)wl[0].w,
+                                 (int)wl[1].x, (int)wl[1].y, (int)wl[1].z, (int)wl[1].w};
+              // both operands e4m3 (format codes 0), no block scales
+              acc[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8v, b8v, acc[t], 0, 0, 0, 0, 0, 0);
+            }
+          } else if (kst < c0 + nst) {
             const uint16_t* arow = lds + r * xstride;
             bf16x8 av[4];
 #pragma unroll
@@ -651,6 +749,16 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
       }
     }
 
+    if constexpr (F8) {
+      // FP8WeightAct.linear's result: bf16(acc * x_scale[m] * w_scale[n]) (fp8.py:48-61,
+      // torch._scaled_mm's epilogue)
+#pragma unroll
+      for (int t = 0; t < NR; ++t) {
+        const float sw = sd_to_f32<MIQ_F32>(load_sd_raw<MIQ_F32>(sbase, row[t]));
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[t][v] = bf16r(acc[t][v] * s_xs[g * 4 + v] * sw);
+      }
+    }
     if constexpr (I8) {
       // int8_wo.linear's result: bf16(bf16(x @ q^T) * bf16(scale)) per row (int8_wo.py:17-21)
 #pragma unroll
@@ -704,7 +812,8 @@ void launch_stream_mode(const MoeParams& p, int grid, size_t lds, int blocks, in
 // fit. MIQ_MOE_WAVES=4 forces four wavefronts.
 template <int KIND, int MODE, bool HZ, int SD, bool G1>
 void launch_stream_gemm(const MoeParams& p, int max_tiles, hipStream_t st) {
-  const size_t lds = (size_t)kTile * (kMoeChunk * kStepK + 8) * 2 + (size_t)kMoeChunk * kTile * 4;
+  const size_t lds = (KIND == KIND_FP8 ? (size_t)kTile * kF8Row : (size_t)kTile * (kMoeChunk * kStepK + 8) * 2) +
+                     (size_t)kMoeChunk * kTile * 4;
   const int K = MODE == MOE_GU ? p.H : p.I;
   const int ng = K / kStepK / p.group_steps;
   constexpr bool kSL16 = KIND == KIND_INT4 && SD != MIQ_F32;
@@ -876,8 +985,11 @@ int run_moe(int kind, const void* hidden, int64_t T, int64_t H, int64_t I, int64
             const void* dn_scale, const void* dn_zero, int sz_dtype, int64_t group, const void* topk_weights,
             int w_dtype, const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* num_padded,
             void* workspace, size_t workspace_bytes, void* out, void* stream, const char* name) {
-  const bool i8 = kind == KIND_INT8;
+  const bool f8 = kind == KIND_FP8;
+  const bool i8 = kind == KIND_INT8 || f8;  // one byte per code, one scale per weight row
   MIQ_REQUIRE(sz_dtype == MIQ_F32 || sz_dtype == MIQ_BF16 || sz_dtype == MIQ_F16, "%s: bad scale dtype", name);
+  MIQ_REQUIRE(!f8 || (sz_dtype == MIQ_F32 && H <= kMoeChunk * kStepK && I <= kMoeChunk * kStepK),
+              "%s: FP8 experts take fp32 scales and H, I of at most %d", name, kMoeChunk * kStepK);
   MIQ_REQUIRE(w_dtype == MIQ_F32 || w_dtype == MIQ_BF16 || w_dtype == MIQ_F16, "%s: bad routing weight dtype", name);
   MIQ_REQUIRE(topk <= kMaxCombineK, "%s: topk=%lld above %d", name, (long long)topk, kMaxCombineK);
   MIQ_REQUIRE(i8 || (group >= kStepK && group % kStepK == 0 && H % group == 0 && I % group == 0),
@@ -925,7 +1037,9 @@ int run_moe(int kind, const void* hidden, int64_t T, int64_t H, int64_t I, int64
   p.out = static_cast<uint16_t*>(out);
   const unsigned tiles = (unsigned)((max_rows + kTile - 1) / kTile);
   hipStream_t st = (hipStream_t)stream;
-  if (i8) {
+  if (f8) {
+    launch_stream_experts_g<KIND_FP8, false, MIQ_F32, false>(p, (int)tiles, st);
+  } else if (i8) {
     if (sz_dtype == MIQ_BF16) launch_stream_experts_g<KIND_INT8, false, MIQ_BF16, false>(p, (int)tiles, st);
     else if (sz_dtype == MIQ_F16) launch_stream_experts_g<KIND_INT8, false, MIQ_F16, false>(p, (int)tiles, st);
     else launch_stream_experts_g<KIND_INT8, false, MIQ_F32, false>(p, (int)tiles, st);
@@ -963,6 +1077,16 @@ extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I
   return run_moe(KIND_INT4, hidden, T, H, I, E, topk, gu_q, gu_scale, gu_zero, dn_q, dn_scale, dn_zero, sz_dtype,
                  group, topk_weights, w_dtype, sorted_ids, expert_ids, num_padded, workspace, workspace_bytes, out,
                  stream, "w4a16_moe");
+}
+
+extern "C" int miq_fp8_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
+                           const uint8_t* gu_q, const float* gu_scale, const uint8_t* dn_q, const float* dn_scale,
+                           const void* topk_weights, int w_dtype, const int32_t* sorted_ids,
+                           const int32_t* expert_ids, const int32_t* num_padded, void* workspace,
+                           size_t workspace_bytes, void* out, void* stream) {
+  return run_moe(KIND_FP8, hidden, T, H, I, E, topk, gu_q, gu_scale, nullptr, dn_q, dn_scale, nullptr, MIQ_F32, 0,
+                 topk_weights, w_dtype, sorted_ids, expert_ids, num_padded, workspace, workspace_bytes, out, stream,
+                 "fp8_moe");
 }
 
 extern "C" int miq_w8a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,

@@ -6,8 +6,8 @@ INT4, `zero`), prefixed `gate_up_` / `down_` for experts, so state dicts and cac
 are interchangeable; `forward` signatures are the reference's.
 
 `QuantExperts.forward` (modules.py:55-75) takes the fused MoE kernels when the experts
-are INT4 or INT8 with a SiLU gate on a ROCm device. Otherwise (FP8 experts, other gates,
-the CPU) it groups the (token, slot)
+are INT4, INT8 or native FP8 with a SiLU gate on a ROCm device. Otherwise (other gates,
+emulated FP8, FP8 layers wider than 2048, the CPU) it groups the (token, slot)
 pairs by expert with one sort and runs every hit expert through `method.linear`. The
 numerics are the reference loop's: gate/up and down in the compute dtype, the product
 with the routing weight in the weights' own dtype, and the results added in ascending
@@ -16,9 +16,10 @@ expert order into a zeroed output of the hidden dtype.
 import torch
 from torch import nn
 
+from engine.quantization.fp8 import FP8WeightAct
 from engine.quantization.int4_wo import Int4WeightOnly
 from engine.quantization.int8_wo import Int8WeightOnly
-from kernels.fused_moe import fused_moe_int4, fused_moe_int8
+from kernels.fused_moe import fused_moe_fp8, fused_moe_int4, fused_moe_int8
 
 
 class _QuantTensors:
@@ -73,8 +74,9 @@ class QuantExperts(_QuantTensors, nn.Module):
 
     def _fused_ok(self, hidden_states):
         """The fused kernels' contract: bf16 activations on the device, a SiLU gate, and INT4
-        codes in groups that are whole multiples of 128 dividing H and I, or INT8 codes with
-        H and I multiples of 128."""
+        codes in groups that are whole multiples of 128 dividing H and I, INT8 codes with
+        H and I multiples of 128, or native FP8 codes with H and I multiples of 128 of at
+        most 2048 (a whole activation row is quantized in one staging)."""
         m = self.method
         if hidden_states.device.type != "cuda" or hidden_states.dtype != torch.bfloat16:
             return False
@@ -87,6 +89,9 @@ class QuantExperts(_QuantTensors, nn.Module):
         if isinstance(m, Int8WeightOnly):
             inter = self.down_qweight.shape[-1]
             return hidden % 128 == 0 and inter % 128 == 0
+        if isinstance(m, FP8WeightAct):
+            inter = self.down_qweight.shape[-1]
+            return m.native and hidden % 128 == 0 and inter % 128 == 0 and hidden <= 2048 and inter <= 2048
         return False
 
     def forward(self, hidden_states, top_k_index, top_k_weights):
@@ -94,6 +99,9 @@ class QuantExperts(_QuantTensors, nn.Module):
             if isinstance(self.method, Int8WeightOnly):
                 return fused_moe_int8(hidden_states, top_k_index, top_k_weights, self.gate_up_qweight,
                                       self.gate_up_scale, self.down_qweight, self.down_scale)
+            if isinstance(self.method, FP8WeightAct):
+                return fused_moe_fp8(hidden_states, top_k_index, top_k_weights, self.gate_up_qweight,
+                                     self.gate_up_scale, self.down_qweight, self.down_scale)
             return fused_moe_int4(hidden_states, top_k_index, top_k_weights,
                                   self.gate_up_qweight, self.gate_up_scale, getattr(self, "gate_up_zero", None),
                                   self.down_qweight, self.down_scale, getattr(self, "down_zero", None))

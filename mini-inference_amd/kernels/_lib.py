@@ -15,7 +15,7 @@ _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.environ.get("MIQ_LIB", os.path.join(_PKG_DIR, "libmiq.so"))
 
 MIQ_F32, MIQ_BF16, MIQ_F16, MIQ_FP8_E4M3, MIQ_INT8, MIQ_UINT8, MIQ_INT32, MIQ_INT64 = range(8)
-ABI_VERSION = 2  # miq_abi_version() of the library these signatures describe
+ABI_VERSION = 3  # miq_abi_version() of the library these signatures describe
 
 _DTYPE_CODES = {
     torch.float32: MIQ_F32,
@@ -55,6 +55,7 @@ SIGNATURES = {
     "miq_moe_workspace_bytes": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "miq_w8a16_moe": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I32, _P, _I32, _P, _P, _P, _P, _SZ,
                              _P, _P]),
+    "miq_fp8_moe": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _SZ, _P, _P]),
     "miq_w4a16_moe": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I32, _I64, _P,
                              _I32, _P, _P, _P, _P, _SZ, _P, _P]),
 }

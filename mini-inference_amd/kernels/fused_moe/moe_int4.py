@@ -1,4 +1,4 @@
-"""Torch-facing wrappers of miq_moe_align, miq_w4a16_moe and miq_w8a16_moe.
+"""Torch-facing wrappers of miq_moe_align, miq_w4a16_moe, miq_w8a16_moe and miq_fp8_moe.
 
 moe_align keeps the contract of the reference (kernels/fused_moe/fused_moe_triton.py:8-39
 and csrc/moe_align.cu:5-88): (sorted_ids, expert_ids, num_padded) with the pairs of each
@@ -81,6 +81,32 @@ def fused_moe_int8(hidden, topk_ids, topk_weights, gu_q, gu_scale, dn_q, dn_scal
     gs, ds = gu_scale.contiguous(), dn_scale.contiguous()
     L.call("miq_w8a16_moe", L.ptr(h), T, H, inter, E, k, L.ptr(gu_q.contiguous()), L.ptr(gs),
            L.ptr(dn_q.contiguous()), L.ptr(ds), L.dtype_code(gs.dtype), L.ptr(w), L.dtype_code(w.dtype),
+           L.ptr(sorted_ids), L.ptr(expert_ids), L.ptr(num_padded), L.ptr(ws), nbytes, L.ptr(out),
+           L.stream(hidden.device))
+    return out
+
+
+def fused_moe_fp8(hidden, topk_ids, topk_weights, gu_q, gu_scale, dn_q, dn_scale):
+    """The FP8 twin of fused_moe_int4: every expert linear is FP8WeightAct.linear on a
+    native device (fp8.py:48-61): the activation rows quantized per row to e4m3 with
+    s = amax / 448, then bf16(sum(x_q w_q) * s_x * s_w). gu_q float8_e4m3fn [E, 2I, H],
+    gu_scale fp32 [E, 2I]; dn_q float8_e4m3fn [E, H, I], dn_scale fp32 [E, H]; H and I
+    multiples of 128 and at most 2048."""
+    L.require_device(hidden, topk_ids, topk_weights, gu_q, dn_q, gu_scale, dn_scale)
+    T, H = hidden.shape
+    E, two_i, _ = gu_q.shape
+    inter = two_i // 2
+    k = topk_ids.shape[-1]
+    if gu_scale.dtype != torch.float32 or dn_scale.dtype != torch.float32:
+        raise RuntimeError("fused_moe_fp8: scales must be float32")
+    sorted_ids, expert_ids, num_padded = moe_align(topk_ids, E, BLOCK_M)
+    h = hidden.contiguous()
+    w = topk_weights.contiguous()
+    nbytes = L.load().miq_moe_workspace_bytes(T, k, E, H, inter)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=hidden.device)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device=hidden.device)
+    L.call("miq_fp8_moe", L.ptr(h), T, H, inter, E, k, L.ptr(gu_q.contiguous()), L.ptr(gu_scale.contiguous()),
+           L.ptr(dn_q.contiguous()), L.ptr(dn_scale.contiguous()), L.ptr(w), L.dtype_code(w.dtype),
            L.ptr(sorted_ids), L.ptr(expert_ids), L.ptr(num_padded), L.ptr(ws), nbytes, L.ptr(out),
            L.stream(hidden.device))
     return out

@@ -45,7 +45,7 @@ def test_ctypes_table_matches_header():
 def test_abi_version_and_error_string():
     from kernels import _lib
     lib = _lib.load()
-    assert lib.miq_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.miq_abi_version() == _lib.ABI_VERSION == 3
     assert lib.miq_tuning_reload() == 0
     # a shape error is reported without touching the GPU
     rc = lib.miq_w8a16_gemm(None, 0, None, None, 0, None, 0, 0, 16, 128, None, 0, None)

@@ -194,6 +194,62 @@ def test_fused_int8_moe_matches_reference_loop(T, H, I, E, k, wdtype):
     assert (err <= 1e-2 + 2e-2 * loop.abs()).all(), err.max().item()
 
 
+def _fp8_native_linear(x, qweight, scale):
+    """FP8WeightAct.linear on a native device (fp8.py:48-61): per-row activation quantize,
+    then torch._scaled_mm's fp32 product times both scales, rounded to the input dtype."""
+    x2d = x.reshape(-1, x.shape[-1])
+    x_fp8, x_scale = O.fp8_quantize_activation(x2d)
+    return O.fp8_scaled_mm(x_fp8, x_scale, qweight, scale).to(x.dtype).reshape(*x.shape[:-1], -1)
+
+
+@pytest.mark.parametrize("T,H,I,E,k", [(64, 2048, 1024, 64, 8), (5, 256, 128, 8, 2), (33, 512, 256, 6, 3),
+                                       (1, 2048, 1024, 64, 8), (40, 1024, 2048, 16, 4)])
+@pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32])
+def test_fused_fp8_moe_matches_reference_loop(T, H, I, E, k, wdtype):
+    """FP8 experts (FP8WeightAct: e4m3fn codes, fp32 per-row scales): the fused layer
+    against the reference loop (modules.py:55-75) with the native FP8 linear on the same
+    codes. The activation codes and scales are the reference's exactly; the products
+    differ in fp32 summation order, and a gate/up output one bf16 step apart can move a
+    down-projection activation code, so the bound is the INT8 layer's."""
+    from kernels.fused_moe import fused_moe_fp8
+    case(f"fused fp8 moe T={T} H={H} I={I} E={E} k={k} weights {wdtype}")
+    g = torch.Generator().manual_seed(25)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
+    wdn = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)
+    gu, dn = O.fp8_quantize(wgu), O.fp8_quantize(wdn)
+    hidden, w, idx = routed(T, H, E, k, seed=26)
+    if wdtype == torch.float32:
+        router = (torch.randn(E, H, generator=g) * 0.02).to(torch.bfloat16)
+        w = torch.softmax(hidden.float() @ router.float().t(), dim=-1).gather(1, idx)
+    loop = MO.quant_experts_loop(hidden, _fp8_native_linear, gu, dn, idx, w, E).float()
+    got = fused_moe_fp8(hidden.to(DEV), idx.to(DEV), w.to(DEV), gu["qweight"].to(DEV), gu["scale"].to(DEV),
+                        dn["qweight"].to(DEV), dn["scale"].to(DEV)).float().cpu()
+    err = (got - loop).abs()
+    print(f"[bound] fp8 moe T={T} {wdtype}: max |fused - reference loop| {err.max().item():.4f}, "
+          f"rel {rel_error(got, loop):.2e}", flush=True)
+    assert rel_error(got, loop) < 1e-2
+    assert (err <= 1e-2 + 2e-2 * loop.abs()).all(), err.max().item()
+
+
+def test_fused_fp8_moe_padding_ids_and_empty_tokens():
+    """Slots routed to expert id E add nothing; a token with every slot padded gets zeros."""
+    from kernels.fused_moe import fused_moe_fp8
+    case("fused fp8 moe padding ids")
+    T, H, I, E, k = 48, 512, 256, 8, 4
+    g = torch.Generator().manual_seed(27)
+    gu = O.fp8_quantize((torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16))
+    dn = O.fp8_quantize((torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16))
+    hidden, w, idx = routed(T, H, E, k, seed=28)
+    idx = idx.clone()
+    idx[::3, 0] = E
+    idx[1::7, :] = E
+    loop = MO.quant_experts_loop(hidden, _fp8_native_linear, gu, dn, idx, w, E).float()
+    got = fused_moe_fp8(hidden.to(DEV), idx.to(DEV), w.to(DEV), gu["qweight"].to(DEV), gu["scale"].to(DEV),
+                        dn["qweight"].to(DEV), dn["scale"].to(DEV)).float().cpu()
+    assert (got[1::7] == 0).all()
+    assert rel_error(got, loop) < 1e-2
+
+
 def test_quant_experts_int8_takes_the_fused_path():
     """QuantExperts with Int8WeightOnly on the device runs the fused kernels (no host loop)
     and matches its own grouped per-expert path."""
@@ -212,6 +268,31 @@ def test_quant_experts_int8_takes_the_fused_path():
     E, H, I, T, k = 16, 512, 256, 24, 4
     qe = QuantExperts(Experts(E, H, I).to(DEV), get_method("int8_wo", device=DEV))
     hidden, w, idx = routed(T, H, E, k, seed=18)
+    hd, wd, idd = hidden.to(DEV), w.to(DEV), idx.to(DEV)
+    assert qe._fused_ok(hd)
+    fused = qe(hd, idd, wd)
+    grouped = qe._grouped(hd, idd, wd)
+    assert rel_error(fused, grouped) < 1e-2
+
+
+def test_quant_experts_fp8_takes_the_fused_path():
+    """QuantExperts with native FP8WeightAct on the device runs the fused kernels (no host
+    loop) and matches its own grouped per-expert path (method.linear per expert)."""
+    from engine.quantization import get_method
+    from engine.quantization.modules import QuantExperts
+    case("QuantExperts fp8 fused vs grouped")
+
+    class Experts(torch.nn.Module):
+        def __init__(self, E, H, I):
+            super().__init__()
+            g = torch.Generator().manual_seed(29)
+            self.gate_up_proj = torch.nn.Parameter((torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16))
+            self.down_proj = torch.nn.Parameter((torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16))
+            self.act_fn = torch.nn.SiLU()
+
+    E, H, I, T, k = 16, 512, 256, 24, 4
+    qe = QuantExperts(Experts(E, H, I).to(DEV), get_method("fp8", device=DEV))
+    hidden, w, idx = routed(T, H, E, k, seed=30)
     hd, wd, idd = hidden.to(DEV), w.to(DEV), idx.to(DEV)
     assert qe._fused_ok(hd)
     fused = qe(hd, idd, wd)
