@@ -231,7 +231,7 @@ int miq_w8a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E
  * rows quantized per row to e4m3fn with s = max(amax, 1e-12) / 448, then
  * bf16(sum(x_q w_q) * s_x * s_w) as torch._scaled_mm returns it.
  * gate_up q: e4m3fn bytes [E, 2I, H], scale fp32 [E, 2I]; down q: e4m3fn bytes [E, H, I],
- * scale fp32 [E, H]. H and I multiples of 128 and at most 2048; sorted_ids / expert_ids /
+ * scale fp32 [E, H]. H and I multiples of 128 and at most 4096; sorted_ids / expert_ids /
  * num_padded from miq_moe_align with block_m == 16; workspace from
  * miq_moe_workspace_bytes. out: bf16 [T, H]. */
 int miq_fp8_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,

@@ -366,10 +366,12 @@ enum { MOE_GU = 0, MOE_DN = 1 };
 constexpr int kMoeD = 2;
 constexpr int kMoeChunk = 16;  // k-steps of activations staged at once
 // FP8 experts (e4m3fn codes, one fp32 scale per weight row), next to wo_core's INT8 / INT4;
-// their activation rows are staged whole (K <= kMoeChunk k-steps) as e4m3 codes with a
-// per-row scale, at this LDS row pitch (16 rows read 16 bytes at one column on distinct banks)
+// their activation rows are staged whole (K <= kF8Steps k-steps: one byte per code, so twice
+// the k-steps of a bf16 chunk in about the same LDS) as e4m3 codes with a per-row scale, at
+// this LDS row pitch (16 rows read 16 bytes at one column on distinct banks)
 constexpr int KIND_FP8 = 2;
-constexpr int kF8Row = kMoeChunk * kStepK + 16;
+constexpr int kF8Steps = 2 * kMoeChunk;
+constexpr int kF8Row = kF8Steps * kStepK + 16;
 
 // SL (16-bit scales, at most kMoeLdsGroups groups per row, a multiple of 4): at the start
 // of an item each lane loads the scale and zero words of its row's groups 4 g .. 4 g + 3
@@ -426,7 +428,8 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
 
   // a workgroup takes runs of `run` consecutive items: they share a tile, so when the
   // whole K fits one chunk its activations are staged once per run
-  const bool one_chunk = steps <= kMoeChunk;
+  constexpr int kChunk = F8 ? kF8Steps : kMoeChunk;  // k-steps staged at once
+  const bool one_chunk = steps <= kChunk;
   int staged_tile = -1;
   if (MODE == MOE_GU)  // every pair starts unranked (-1); the down kernel ranks the routed ones
     for (int i = blockIdx.x * kThreads + tid; i < p.num_pairs; i += gridDim.x * kThreads) p.rank[i] = -1;
@@ -542,8 +545,8 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
     xsg = z4;
     int c_grp = 0, c_left = p.group_steps;  // group of the next k-step and its steps left
 
-    for (int c0 = 0; c0 < steps; c0 += kMoeChunk) {
-      const int nst = min(kMoeChunk, steps - c0);
+    for (int c0 = 0; c0 < steps; c0 += kChunk) {
+      const int nst = min(kChunk, steps - c0);
       const int xcols = nst * (kStepK / 8);
       const int npieces = kTile * xcols;
       if (c0) __syncthreads();
@@ -812,8 +815,8 @@ void launch_stream_mode(const MoeParams& p, int grid, size_t lds, int blocks, in
 // fit. MIQ_MOE_WAVES=4 forces four wavefronts.
 template <int KIND, int MODE, bool HZ, int SD, bool G1>
 void launch_stream_gemm(const MoeParams& p, int max_tiles, hipStream_t st) {
-  const size_t lds = (KIND == KIND_FP8 ? (size_t)kTile * kF8Row : (size_t)kTile * (kMoeChunk * kStepK + 8) * 2) +
-                     (size_t)kMoeChunk * kTile * 4;
+  const size_t lds = KIND == KIND_FP8 ? (size_t)kTile * kF8Row + (size_t)kF8Steps * kTile * 4
+                                      : (size_t)kTile * (kMoeChunk * kStepK + 8) * 2 + (size_t)kMoeChunk * kTile * 4;
   const int K = MODE == MOE_GU ? p.H : p.I;
   const int ng = K / kStepK / p.group_steps;
   constexpr bool kSL16 = KIND == KIND_INT4 && SD != MIQ_F32;
@@ -988,8 +991,8 @@ int run_moe(int kind, const void* hidden, int64_t T, int64_t H, int64_t I, int64
   const bool f8 = kind == KIND_FP8;
   const bool i8 = kind == KIND_INT8 || f8;  // one byte per code, one scale per weight row
   MIQ_REQUIRE(sz_dtype == MIQ_F32 || sz_dtype == MIQ_BF16 || sz_dtype == MIQ_F16, "%s: bad scale dtype", name);
-  MIQ_REQUIRE(!f8 || (sz_dtype == MIQ_F32 && H <= kMoeChunk * kStepK && I <= kMoeChunk * kStepK),
-              "%s: FP8 experts take fp32 scales and H, I of at most %d", name, kMoeChunk * kStepK);
+  MIQ_REQUIRE(!f8 || (sz_dtype == MIQ_F32 && H <= kF8Steps * kStepK && I <= kF8Steps * kStepK),
+              "%s: FP8 experts take fp32 scales and H, I of at most %d", name, kF8Steps * kStepK);
   MIQ_REQUIRE(w_dtype == MIQ_F32 || w_dtype == MIQ_BF16 || w_dtype == MIQ_F16, "%s: bad routing weight dtype", name);
   MIQ_REQUIRE(topk <= kMaxCombineK, "%s: topk=%lld above %d", name, (long long)topk, kMaxCombineK);
   MIQ_REQUIRE(i8 || (group >= kStepK && group % kStepK == 0 && H % group == 0 && I % group == 0),

@@ -7,7 +7,7 @@ are interchangeable; `forward` signatures are the reference's.
 
 `QuantExperts.forward` (modules.py:55-75) takes the fused MoE kernels when the experts
 are INT4, INT8 or native FP8 with a SiLU gate on a ROCm device. Otherwise (other gates,
-emulated FP8, FP8 layers wider than 2048, the CPU) it groups the (token, slot)
+emulated FP8, FP8 layers wider than 4096, the CPU) it groups the (token, slot)
 pairs by expert with one sort and runs every hit expert through `method.linear`. The
 numerics are the reference loop's: gate/up and down in the compute dtype, the product
 with the routing weight in the weights' own dtype, and the results added in ascending
@@ -76,7 +76,7 @@ class QuantExperts(_QuantTensors, nn.Module):
         """The fused kernels' contract: bf16 activations on the device, a SiLU gate, and INT4
         codes in groups that are whole multiples of 128 dividing H and I, INT8 codes with
         H and I multiples of 128, or native FP8 codes with H and I multiples of 128 of at
-        most 2048 (a whole activation row is quantized in one staging)."""
+        most 4096 (a whole activation row is quantized in one staging)."""
         m = self.method
         if hidden_states.device.type != "cuda" or hidden_states.dtype != torch.bfloat16:
             return False
@@ -91,7 +91,7 @@ class QuantExperts(_QuantTensors, nn.Module):
             return hidden % 128 == 0 and inter % 128 == 0
         if isinstance(m, FP8WeightAct):
             inter = self.down_qweight.shape[-1]
-            return m.native and hidden % 128 == 0 and inter % 128 == 0 and hidden <= 2048 and inter <= 2048
+            return m.native and hidden % 128 == 0 and inter % 128 == 0 and hidden <= 4096 and inter <= 4096
         return False
 
     def forward(self, hidden_states, top_k_index, top_k_weights):

@@ -91,7 +91,7 @@ def fused_moe_fp8(hidden, topk_ids, topk_weights, gu_q, gu_scale, dn_q, dn_scale
     native device (fp8.py:48-61): the activation rows quantized per row to e4m3 with
     s = amax / 448, then bf16(sum(x_q w_q) * s_x * s_w). gu_q float8_e4m3fn [E, 2I, H],
     gu_scale fp32 [E, 2I]; dn_q float8_e4m3fn [E, H, I], dn_scale fp32 [E, H]; H and I
-    multiples of 128 and at most 2048."""
+    multiples of 128 and at most 4096."""
     L.require_device(hidden, topk_ids, topk_weights, gu_q, dn_q, gu_scale, dn_scale)
     T, H = hidden.shape
     E, two_i, _ = gu_q.shape
