@@ -189,10 +189,16 @@ def bench_fp8(dev):
     t_quant = time_graph([lambda: ops.fp8_quantize_rows(x)] * reps) / reps
     tf = flops / t_gemm / 1e12
     tf_all = flops / (t_gemm + t_quant) / 1e12
+    # the library GEMM the reference calls (fp8.py:55-61: torch._scaled_mm with row-wise
+    # scales), on the same operands, in the same graph timing
+    sa, sb = xs.reshape(-1, 1), ws.reshape(1, -1)
+    t_lib = time_graph([lambda: torch._scaled_mm(xq, wq.t(), scale_a=sa, scale_b=sb, out_dtype=torch.bfloat16)]
+                       * reps) / reps
     return {"gemm_us": round(t_gemm * 1e6, 2), "gemm_TFLOP/s": round(tf, 1),
             "pct_fp8_peak": round(100 * tf / FP8_PEAK_TFLOPS, 1),
             "act_quant_us": round(t_quant * 1e6, 2),
-            "quant+gemm_TFLOP/s": round(tf_all, 1), "peak_used_TFLOP/s": FP8_PEAK_TFLOPS}
+            "quant+gemm_TFLOP/s": round(tf_all, 1), "peak_used_TFLOP/s": FP8_PEAK_TFLOPS,
+            "hipblaslt_rowwise_scaled_mm_us": round(t_lib * 1e6, 2)}
 
 
 def attention_tables(B=64, page=16, seed=7):
