@@ -145,13 +145,35 @@ def bench_headline(dev, steps, warmup):
     return cfg, step_bytes, t
 
 
-def per_m(cfg, launch, nbytes, dev, reps_per_graph=40):
+def per_m(cfg, launch, nbytes, dev, reps_per_graph=40, ref_launch=None):
+    """Graph timing per M; with ref_launch, the reference's own formula on the device
+    (dequantize, then the library GEMM) timed the same way beside it."""
     out = {}
     for M in MS:
         t = time_graph([launch(cfg, M, i) for i in range(reps_per_graph)]) / reps_per_graph
         gbs = nbytes(cfg, M) / t / 1e9
         out[f"M={M}"] = {"us": round(t * 1e6, 2), "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1)}
+        if ref_launch is not None:
+            n = 8
+            tr = time_graph([ref_launch(cfg, M, i) for i in range(n)]) / n
+            out[f"M={M}"]["reference_formula_on_device_us"] = round(tr * 1e6, 2)
     return out
+
+
+def int4_ref_launch(cfg, M, i):
+    """int4_wo.py:33-42 + base.py:20-24 on the device: dequantize (the HIP kernel, the
+    reference's two bf16 roundings), then F.linear (hipBLASLt)."""
+    from kernels import quant_ops as ops
+    q, s, z = cfg["copies"][i % len(cfg["copies"])]
+    x = cfg["x"][M]
+    return lambda: torch.nn.functional.linear(x, ops.int4_dequantize(q, s, z).to(x.dtype))
+
+
+def int8_ref_launch(cfg, M, i):
+    """int8_wo.py:17-21 on the device: F.linear(x, q.to(bf16)) * s (hipBLASLt)."""
+    q, s = cfg["copies"][i % len(cfg["copies"])]
+    x = cfg["x"][M]
+    return lambda: torch.nn.functional.linear(x, q.to(x.dtype)) * s.to(x.dtype)
 
 
 def bench_int8(dev):
@@ -164,7 +186,7 @@ def bench_int8(dev):
         return lambda: ops.w8a16_linear(x, q, s)
 
     nbytes = lambda c, M: c["wbytes"] + M * c["K"] * 2 + M * c["N"] * 2  # noqa: E731
-    res = per_m(cfg, launch, nbytes, dev, reps_per_graph=24)
+    res = per_m(cfg, launch, nbytes, dev, reps_per_graph=24, ref_launch=int8_ref_launch)
     del cfg
     return res
 
@@ -584,7 +606,8 @@ def measure_traffic():
 
 
 SECTIONS = {
-    "int4_w4a16_sym_per_M": lambda dev: per_m(int4_setup(dev), int4_launch, int4_bytes, dev),
+    "int4_w4a16_sym_per_M": lambda dev: per_m(int4_setup(dev), int4_launch, int4_bytes, dev,
+                                              ref_launch=int4_ref_launch),
     "int4_w4a16_zero_point_per_M": bench_int4_asym,
     "int8_w8a16_gate_up_per_M": bench_int8,
     "fp8_prefill_gemm": bench_fp8,
