@@ -334,8 +334,13 @@ def bench_moe(dev):
     reps = 12
     t = time_graph([launch(i) for i in range(reps)]) / reps
     gbs = c["bytes"] / t / 1e9
+    from engine.quantization.int4_wo import Int4WeightOnly
+    (gq, gs), (dq, ds) = c["sets"][0]
+    tg = grouped_path_time(Int4WeightOnly(group_size=128), c["E"], {"qweight": gq, "scale": gs},
+                           {"qweight": dq, "scale": ds}, c["hidden"], c["idx"], c["w"])
     res = {"us_per_layer": round(t * 1e6, 2), "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
-           "experts_touched": c["touched"], "MB_per_call": round(c["bytes"] / 1e6, 1)}
+           "experts_touched": c["touched"], "MB_per_call": round(c["bytes"] / 1e6, 1),
+           "grouped_per_expert_path_us": round(tg * 1e6, 1)}
     del c
     return res
 
@@ -365,8 +370,33 @@ def bench_moe_int8(dev):
     reps = 8
     t = time_graph([launch(i) for i in range(reps)]) / reps
     gbs = nbytes / t / 1e9
+    from engine.quantization.int8_wo import Int8WeightOnly
+    gq, gs, dq, ds = sets[0]
+    tg = grouped_path_time(Int8WeightOnly(), E, {"qweight": gq, "scale": gs}, {"qweight": dq, "scale": ds},
+                           hidden, idx, w)
     return {"us_per_layer": round(t * 1e6, 2), "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
-            "experts_touched": touched, "MB_per_call": round(nbytes / 1e6, 1)}
+            "experts_touched": touched, "MB_per_call": round(nbytes / 1e6, 1),
+            "grouped_per_expert_path_us": round(tg * 1e6, 1)}
+
+
+def grouped_path_time(method, E, gate_up, down, hidden, idx, w, reps=5):
+    """Seconds per call of QuantExperts' grouped path: the reference loop's structure
+    (modules.py:55-75: one sort, then method.linear per hit expert) on the device. It syncs
+    with the host inside (the expert list), so it is timed eagerly, not in a graph."""
+    from engine.quantization.modules import QuantExperts
+    qe = QuantExperts.__new__(QuantExperts)
+    torch.nn.Module.__init__(qe)
+    qe.method, qe.num_experts, qe.act_fn = method, E, torch.nn.SiLU()
+    qe._store("gate_up_", gate_up)
+    qe._store("down_", down)
+    for _ in range(2):
+        qe._grouped(hidden, idx, w)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        qe._grouped(hidden, idx, w)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / reps
 
 
 def bench_moe_fp8(dev):
@@ -396,24 +426,10 @@ def bench_moe_fp8(dev):
     reps = 8
     t = time_graph([launch(i) for i in range(reps)]) / reps
     gbs = nbytes / t / 1e9
-    # the grouped path (host loop with a device sync per call: timed eagerly, not in a graph)
     from engine.quantization.fp8 import FP8WeightAct
-    from engine.quantization.modules import QuantExperts
-    method = FP8WeightAct(device=dev)
-    qe = QuantExperts.__new__(QuantExperts)
-    torch.nn.Module.__init__(qe)
-    qe.method, qe.num_experts, qe.act_fn = method, E, torch.nn.SiLU()
     gq, gs, dq, ds = sets[0]
-    qe._store("gate_up_", {"qweight": gq, "scale": gs})
-    qe._store("down_", {"qweight": dq, "scale": ds})
-    for _ in range(2):
-        qe._grouped(hidden, idx, w)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(5):
-        qe._grouped(hidden, idx, w)
-    torch.cuda.synchronize()
-    tg = (time.perf_counter() - t0) / 5
+    tg = grouped_path_time(FP8WeightAct(device=dev), E, {"qweight": gq, "scale": gs}, {"qweight": dq, "scale": ds},
+                           hidden, idx, w)
     return {"us_per_layer": round(t * 1e6, 2), "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
             "experts_touched": touched, "MB_per_call": round(nbytes / 1e6, 1),
             "grouped_per_expert_path_us": round(tg * 1e6, 1)}
