@@ -204,7 +204,7 @@ def _fp8_native_linear(x, qweight, scale):
 
 @pytest.mark.parametrize("T,H,I,E,k", [(64, 2048, 1024, 64, 8), (5, 256, 128, 8, 2), (33, 512, 256, 6, 3),
                                        (1, 2048, 1024, 64, 8), (40, 1024, 2048, 16, 4), (12, 4096, 1536, 8, 2),
-                                       (9, 1152, 4096, 4, 2)])
+                                       (9, 1152, 4096, 4, 2), (7, 384, 256, 4, 2)])
 @pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32])
 def test_fused_fp8_moe_matches_reference_loop(T, H, I, E, k, wdtype):
     """FP8 experts (FP8WeightAct: e4m3fn codes, fp32 per-row scales): the fused layer
