@@ -25,6 +25,18 @@ __host__ __device__ inline float bf16_to_f32(uint16_t h) {
   return v.f;
 }
 
+// x / s rounded to nearest, given r = RN(1 / s): q = RN(x r) is within an ulp of x / s,
+// and then RN(q + RN(x - q s) r) is the correctly rounded quotient (Markstein's theorem;
+// both corrections are fused multiply-adds, so this is three operations instead of the
+// division sequence). Valid while x / s and the residual stay in the normal range, which
+// holds for activation quantization (|x / s| <= 448 up to rounding; results below the
+// normal range become e4m3 zero either way). s > 0, so the quotient carries the sign of x;
+// copying it back keeps -0 / s = -0 (the last add would give +0 there).
+__device__ inline float div_by_recip(float x, float s, float r) {
+  const float q = x * r;
+  return __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-q, s, x), r, q), x);
+}
+
 __host__ __device__ inline uint16_t f32_to_bf16(float f) {
   union { uint32_t u; float f; } v;
   v.f = f;

@@ -393,7 +393,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
   constexpr bool I8 = KIND == KIND_INT8, F8 = KIND == KIND_FP8;
   constexpr bool B1 = I8 || F8;  // one byte per code: a k-step of a tile is two line loads
   constexpr int NR = 2, NL = B1 ? 2 : 1, D = kMoeD;
-  __shared__ float s_xs[kTile];  // FP8: the activation rows' scales
+  __shared__ float s_xs[kTile], s_xr[kTile];  // FP8: the activation rows' scales and their reciprocals
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
   const int K = MODE == MOE_GU ? p.H : p.I;
@@ -590,7 +590,9 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
           if (tid < kTile) {
             float a = 0.f;
             for (int q = 0; q < nst; ++q) a = fmaxf(a, xsum[q * kTile + tid]);
-            s_xs[tid] = fmaxf(a, 1e-12f) / 448.0f;
+            const float sx = fmaxf(a, 1e-12f) / 448.0f;
+            s_xs[tid] = sx;
+            s_xr[tid] = 1.0f / sx;
           }
           __syncthreads();
           uint8_t* a8 = reinterpret_cast<uint8_t*>(lds);
@@ -603,15 +605,18 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
               const int i = base + tid + j * kThreads;
               if (i < npieces) {
                 const int m = i / xcols, c = i - m * xcols;
-                const float sx = s_xs[m];
+                const float sx = s_xs[m], rx = s_xr[m];
+                // x / s correctly rounded without a division (the division sequence cost
+                // 6.5 us of the 92 us OLMoE FP8 layer)
+                auto quot = [&](float x) { return div_by_recip(x, sx, rx); };
                 const uint32_t w4[4] = {xr[j].x, xr[j].y, xr[j].z, xr[j].w};
                 int o[2];
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                  const float v0 = fminf(fmaxf(bf16_to_f32(w4[2 * h] & 0xffff) / sx, -448.f), 448.f);
-                  const float v1 = fminf(fmaxf(bf16_to_f32(w4[2 * h] >> 16) / sx, -448.f), 448.f);
-                  const float v2 = fminf(fmaxf(bf16_to_f32(w4[2 * h + 1] & 0xffff) / sx, -448.f), 448.f);
-                  const float v3 = fminf(fmaxf(bf16_to_f32(w4[2 * h + 1] >> 16) / sx, -448.f), 448.f);
+                  const float v0 = fminf(fmaxf(quot(bf16_to_f32(w4[2 * h] & 0xffff)), -448.f), 448.f);
+                  const float v1 = fminf(fmaxf(quot(bf16_to_f32(w4[2 * h] >> 16)), -448.f), 448.f);
+                  const float v2 = fminf(fmaxf(quot(bf16_to_f32(w4[2 * h + 1] & 0xffff)), -448.f), 448.f);
+                  const float v3 = fminf(fmaxf(quot(bf16_to_f32(w4[2 * h + 1] >> 16)), -448.f), 448.f);
                   o[h] = __builtin_amdgcn_cvt_pk_fp8_f32(v0, v1, 0, false);
                   o[h] = __builtin_amdgcn_cvt_pk_fp8_f32(v2, v3, o[h], true);
                 }

@@ -121,38 +121,55 @@ fp8_quantize_rows_kernel(const void* __restrict__ x, int x_dtype, int64_t K, int
   float amax = 0.f;
   if (x_dtype == MIQ_BF16 && (K % 8) == 0 && (ldx % 8) == 0 &&
       (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+    // the row's 8-element pieces: up to kHeld per thread stay in registers between the
+    // max pass and the conversion pass (K <= 8192 at 256 threads), later ones are read again
+    constexpr int kHeld = 4;
     const uint4* xv = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base);
-    for (int64_t c = threadIdx.x; c < K / 8; c += blockDim.x) {
-      const uint4 p = xv[c];
+    const int64_t npc = K / 8;
+    uint4 held[kHeld];
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) {
+      const int64_t c = threadIdx.x + (int64_t)j * blockDim.x;
+      held[j] = c < npc ? xv[c] : make_uint4(0, 0, 0, 0);
+    }
+    auto piece_max = [&](const uint4& p) {
       const uint32_t d[4] = {p.x, p.y, p.z, p.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         amax = fmaxf(amax, fabsf(bf16_to_f32(d[i] & 0xffff)));
         amax = fmaxf(amax, fabsf(bf16_to_f32(d[i] >> 16)));
       }
-    }
+    };
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) piece_max(held[j]);
+    for (int64_t c = threadIdx.x + (int64_t)kHeld * blockDim.x; c < npc; c += blockDim.x) piece_max(xv[c]);
     amax = block_reduce_max(amax, red);
-    const float s = fmaxf(amax, 1e-12f) / 448.0f;
+    const float s = fmaxf(amax, 1e-12f) / 448.0f, rs = 1.0f / s;
     uint2* qv = reinterpret_cast<uint2*>(q + row * K);
-    for (int64_t c = threadIdx.x; c < K / 8; c += blockDim.x) {
-      const uint4 p = xv[c];
+    // the hardware e4m3 (OCP) conversion rounds to nearest even like f32_to_fp8; the
+    // inputs are clamped to +-448 first, as the reference does
+    auto convert = [&](const uint4& p, int64_t c) {
       const uint32_t d[4] = {p.x, p.y, p.z, p.w};
-      // the hardware e4m3 (OCP) conversion rounds to nearest even like f32_to_fp8; the
-      // inputs are clamped to +-448 first, as the reference does
       int o[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         float v[4];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-          v[2 * i] = fminf(fmaxf(bf16_to_f32(d[2 * h + i] & 0xffff) / s, -448.f), 448.f);
-          v[2 * i + 1] = fminf(fmaxf(bf16_to_f32(d[2 * h + i] >> 16) / s, -448.f), 448.f);
+          v[2 * i] = fminf(fmaxf(div_by_recip(bf16_to_f32(d[2 * h + i] & 0xffff), s, rs), -448.f), 448.f);
+          v[2 * i + 1] = fminf(fmaxf(div_by_recip(bf16_to_f32(d[2 * h + i] >> 16), s, rs), -448.f), 448.f);
         }
         o[h] = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
         o[h] = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], o[h], true);
       }
       qv[c] = make_uint2((uint32_t)o[0], (uint32_t)o[1]);
+    };
+#pragma unroll
+    for (int j = 0; j < kHeld; ++j) {
+      const int64_t c = threadIdx.x + (int64_t)j * blockDim.x;
+      if (c < npc) convert(held[j], c);
     }
+    for (int64_t c = threadIdx.x + (int64_t)kHeld * blockDim.x; c < npc; c += blockDim.x) convert(xv[c], c);
     if (threadIdx.x == 0) scale[row] = s;
     return;
   }
