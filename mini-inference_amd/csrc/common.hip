@@ -20,6 +20,8 @@ Tuning read_tuning() {
   t.wo_stream = flag("MIQ_WO_STREAM");
   const char* rows = getenv("MIQ_WO_ROWS");
   t.wo_rows = rows ? atoi(rows) : 0;
+  const char* pmin = getenv("MIQ_WO_PAIR_MIN_M");
+  t.wo_pair_min_m = pmin ? atoi(pmin) : 0;
   t.wo_msplit_set = pair("MIQ_WO_MSPLIT", t.wo_msplit_nr, t.wo_msplit_s);
   t.wo_plan_set = pair("MIQ_WO_PLAN", t.wo_plan_nr, t.wo_plan_s);
   const char* panel = getenv("MIQ_WO_PANEL");

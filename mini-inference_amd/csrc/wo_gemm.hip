@@ -26,9 +26,10 @@ int wo_prefill_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w
                       const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int64_t M,
                       int N, int K, void* workspace, size_t ws_bytes, size_t counter_bytes, hipStream_t st,
                       const char* name);
+size_t wo_tile_pair_bytes(int64_t M, int64_t N);
 int wo_tile_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, const void* scale,
                    const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int M,
-                   int N, int K, hipStream_t st, const char* name, bool& launched);
+                   int N, int K, void* pair, size_t pair_bytes, hipStream_t st, const char* name, bool& launched);
 
 namespace {
 
@@ -67,8 +68,12 @@ int run(int kind, const WoArgs& p, void* workspace, size_t ws_bytes, hipStream_t
                                    launched);
     if (launched || rc != MIQ_OK) return rc;
   }
+  // the tile kernel's exchange words sit past the counter area of the workspace
+  const bool have = workspace != nullptr && ws_bytes > kWoCounterBytes;
+  void* pair = have ? static_cast<char*>(workspace) + kWoCounterBytes : nullptr;
+  const size_t pair_bytes = have ? ws_bytes - kWoCounterBytes : 0;
   const int rc = wo_tile_launch(kind, p.x, p.ldx, p.w, p.ldw, p.scale, p.zero, p.sz_dtype, p.group_steps, p.ngroups,
-                                p.y, p.ldy, p.M, p.N, p.K, st, name, launched);
+                                p.y, p.ldy, p.M, p.N, p.K, pair, pair_bytes, st, name, launched);
   if (launched || rc != MIQ_OK) return rc;
   return wo_stream_launch(kind, p.x, p.ldx, p.w, p.ldw, p.scale, p.zero, p.sz_dtype, p.group_steps, p.ngroups, p.y,
                           p.ldy, p.M, p.N, p.K, workspace, ws_bytes, st, name);
@@ -84,7 +89,8 @@ extern "C" size_t miq_wo_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, i
                              ? wo_prefill_workspace_bytes(M, N, K, weight_bits, kWoCounterBytes) : 0;
   const size_t stream = wo_stream_workspace_bytes(M, N, K, weight_bits);
   if (weight_bits != 4 || M < 1 || N < 1 || K < kStepK) return std::max({kWoCounterBytes, stream, prefill});
-  return std::max({kWoCounterBytes, stream, prefill, kWoCounterBytes + wo_panel_partial_bytes(M, N, K)});
+  return std::max({kWoCounterBytes, stream, prefill, kWoCounterBytes + wo_panel_partial_bytes(M, N, K),
+                   kWoCounterBytes + wo_tile_pair_bytes(M, N)});
 }
 
 extern "C" int miq_w8a16_gemm(const void* x, int64_t ldx, const int8_t* q, const void* scale,

@@ -16,6 +16,14 @@
 // k-steps per wavefront rather than the bytes per CU (on MI355X an M=1 launch takes about
 // as long with 80 workgroups as with 256; halving K saves a third).
 //
+// INT4 at 7 to 10 rows (where a CU's staged activations outweigh its weights) takes the
+// two-half plan: a workgroup owns two 16-row tiles over half of K, so each CU stages half
+// the activations for the same weight bytes, and the two workgroups of a pair meet in one
+// word per output of the caller's zeroed workspace. Each swaps its fp32 sum in with one
+// agent-scope atomic exchange; the one that finds the other's sum adds the two (the same
+// bits in either order), writes y and clears the word, so there is one round trip and no
+// counter, and the workspace is all zeros again after the call.
+//
 // Per-element math is the one of the streamed kernel (wo_stream.hip): codes unpack to
 // bf16 128 + code, MFMA 16x16x32 bf16 with fp32 accumulation, and per quantization group
 // acc += s * (sum x (128 + code) + bias * sum x) (bias -136 for symmetric int4 codes, -128
@@ -48,6 +56,12 @@ using namespace wo;
 constexpr int kTileNS = 8;                 // k-steps in flight per wavefront (all of its slice)
 constexpr int kTileLds = 160 * 1024;       // gfx950 LDS per workgroup
 constexpr int kCUs = 256;                  // MI355X compute units
+// int4: rows of the two-half plan by default. INT4 N = 2560, K = 9728 on MI355X, weights
+// read from HBM (rotating copies), one tile over all of K (M > 8: the streamed kernel)
+// against two halves: M = 1 / 4 / 6 / 8 / 10 / 12 / 16 took 6.4 / 8.0 / 9.3 / 10.8 / 11.5 /
+// 12.0 / 12.8 us against 7.6 / 8.7 / 9.5 / 10.25 / 11.3 / 12.3 / 13.9 us: the exchange costs
+// about 1 us and pays at 8 to 10 rows, where a CU's staged activations outweigh its weights
+constexpr int kPairMinM = 7, kPairMaxM = 10;
 // activation pieces (16 B) per lane per round (int8 holds twice the weight registers):
 // 12 x 64 pieces cover a wavefront's slice at M = 8 (8 rows x 6 k-steps) in one round;
 // 16 measured slower (register pressure)
@@ -68,12 +82,18 @@ struct TileParams {
   int M, N, steps;      // steps = K / 128
   int rows;             // weight rows per tile (1..16)
   int units, unit_steps;
+  int xsteps;           // k-steps of activations staged per workgroup (its K range)
+  uint32_t* pair;       // two-half workgroups: [M][N] exchange words, all zero between calls
   int wbytes, sbytes;
 };
 
-template <int KIND, bool HZ, int SD, int W, bool G1>
+// NT row tiles of 16 rows per workgroup; KS = 2 gives each tile two workgroups, one per
+// half of K (workgroup 2 t + h takes half h of tile t), whose fp32 results meet in one
+// exchange word per output (below).
+template <int KIND, bool HZ, int SD, int W, bool G1, int NT, int KS>
 __global__ void __launch_bounds__(W * 64)
 wo_tile_kernel(TileParams p) {
+  static_assert(KIND == KIND_INT4 || (NT == 1 && KS == 1), "int8 takes one row tile over all of K");
   constexpr int kThreads = W * 64, NS = kTileNS, XP = tile_xp<KIND>();
   constexpr int kStepBytes = KIND == KIND_INT4 ? kStepK / 2 : kStepK;  // per weight row
   extern __shared__ __align__(16) uint16_t lds[];
@@ -83,8 +103,13 @@ wo_tile_kernel(TileParams p) {
   const int M = p.M;
   MIQ_TRACE(0);
 
-  // this wavefront's slice of K, in whole units (groups, or pairs of them)
-  const int u0 = p.units * wv / W, u1 = p.units * (wv + 1) / W;
+  // the workgroup's K range (units ua .. ub; LDS holds it from k-step kb on), then this
+  // wavefront's slice of it, in whole units (groups, or pairs of them)
+  const int half = KS == 2 ? (int)(blockIdx.x & 1) : 0;
+  const int tile = KS == 2 ? (int)(blockIdx.x >> 1) : (int)blockIdx.x;
+  const int ua = p.units * half / KS, ub = p.units * (half + 1) / KS;
+  const int kb = ua * p.unit_steps;
+  const int u0 = ua + (ub - ua) * wv / W, u1 = ua + (ub - ua) * (wv + 1) / W;
   const int st0 = u0 * p.unit_steps, nst = (u1 - u0) * p.unit_steps;
 
   // ---- activation loads first: each wavefront stages the M rows of its own slice of K
@@ -110,20 +135,24 @@ wo_tile_kernel(TileParams p) {
   load_x(0);
   MIQ_TRACE(5);
 
-  // ---- then every weight and scale word of the slice
-  const int n0 = blockIdx.x * p.rows;
-  const int nrow = n0 + r;
-  const int nrows = min(p.rows, p.N - n0);  // rows of this tile that exist
+  // ---- then every weight and scale word of the slice (row tile t: rows n0 + 16 t ..)
+  const int n0 = tile * p.rows * NT;
+  int nrows[NT];  // rows of each row tile that exist
+#pragma unroll
+  for (int t = 0; t < NT; ++t) nrows[t] = min(p.rows, p.N - n0 - 16 * t);
   // load h: lane 32 c2 + 4 rr + cl reads row 8h + rr, bytes 64 c2 + 16 cl of the k-step pair
   const int lrr = (lane >> 2) & 7, lcl = lane & 3, lc2 = lane >> 5;
-  int woff[2], wok[2];
+  int woff[NT][2], wok[NT][2], soff[NT];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    woff[h] = min(n0 + 8 * h + lrr, p.N - 1) * (int)p.ldw + st0 * kStepBytes + lc2 * 64 + lcl * 16;
-    wok[h] = (8 * h + lrr - nrows) >> 31;  // all ones for a row of the tile
+  for (int t = 0; t < NT; ++t) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      woff[t][h] = min(n0 + 16 * t + 8 * h + lrr, p.N - 1) * (int)p.ldw + st0 * kStepBytes + lc2 * 64 + lcl * 16;
+      wok[t][h] = (8 * h + lrr - nrows[t]) >> 31;  // all ones for a row of the tile
+    }
+    soff[t] = (int)(min(n0 + 16 * t + r, p.N - 1) * p.ngroups + st0 / p.group_steps);
   }
   const int bp_addr = (32 * (r >> 3) + 4 * (r & 7) + g) * 4;
-  const int soff = (int)(min(nrow, p.N - 1) * p.ngroups + st0 / p.group_steps);
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(p.w), 0, p.wbytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p.scale), 0, p.sbytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t zrs =
@@ -142,40 +171,47 @@ wo_tile_kernel(TileParams p) {
   // the weights: the multiply of k-step d then waits only for the weight loads up to d
   // (loads complete in issue order), not for the last one
   constexpr int esz = SD == MIQ_F32 ? 4 : 2;
-  uint32_t sw[8], zw[8];
-  const int sbase = r < nrows ? (soff * esz) & ~3 : kOut - 32;
+  uint32_t sw[NT][8], zw[NT][8];
   if (KIND == KIND_INT4) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(srs, sbase + 16 * h, 0, 0);
-      const uint4 u = *reinterpret_cast<const uint4*>(&v);
-      sw[4 * h] = u.x; sw[4 * h + 1] = u.y; sw[4 * h + 2] = u.z; sw[4 * h + 3] = u.w;
-      if (HZ) {
-        const auto vz = __builtin_amdgcn_raw_buffer_load_b128(zrs, sbase + 16 * h, 0, 0);
-        const uint4 uz = *reinterpret_cast<const uint4*>(&vz);
-        zw[4 * h] = uz.x; zw[4 * h + 1] = uz.y; zw[4 * h + 2] = uz.z; zw[4 * h + 3] = uz.w;
+    for (int t = 0; t < NT; ++t) {
+      const int sbase = r < nrows[t] ? (soff[t] * esz) & ~3 : kOut - 32;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(srs, sbase + 16 * h, 0, 0);
+        const uint4 u = *reinterpret_cast<const uint4*>(&v);
+        sw[t][4 * h] = u.x; sw[t][4 * h + 1] = u.y; sw[t][4 * h + 2] = u.z; sw[t][4 * h + 3] = u.w;
+        if (HZ) {
+          const auto vz = __builtin_amdgcn_raw_buffer_load_b128(zrs, sbase + 16 * h, 0, 0);
+          const uint4 uz = *reinterpret_cast<const uint4*>(&vz);
+          zw[t][4 * h] = uz.x; zw[t][4 * h + 1] = uz.y; zw[t][4 * h + 2] = uz.z; zw[t][4 * h + 3] = uz.w;
+        }
       }
     }
   }
-  // int4: raw loads of k-steps d, d + 1 (d even) in wq[d], wq[d + 1]; int8: wq[d][0..1]
+  // int4: raw loads of k-steps d, d + 1 (d even) in wq[t][d], wq[t][d + 1]; int8: wq[t][d][0..1]
   constexpr int NL = KIND == KIND_INT4 ? 1 : 2;
-  uint4 wq[NS][NL];
+  uint4 wq[NT][NS][NL];
 #pragma unroll
   for (int d = 0; d < NS; ++d) {
     if (KIND == KIND_INT8 || (d & 1) == 0) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int kp = ((d + (KIND == KIND_INT4 ? lc2 : 0) - nsteps_v) >> 31) & wok[h];
-        const int off = ((woff[h] + d * kStepBytes) & kp) | (kOut & ~kp);
-        const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2 /* nt */);
-        if (KIND == KIND_INT4) wq[d + h][0] = *reinterpret_cast<const uint4*>(&v);
-        else wq[d][h] = *reinterpret_cast<const uint4*>(&v);
+      for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int kp = ((d + (KIND == KIND_INT4 ? lc2 : 0) - nsteps_v) >> 31) & wok[t][h];
+          const int off = ((woff[t][h] + d * kStepBytes) & kp) | (kOut & ~kp);
+          const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 2 /* nt */);
+          if (KIND == KIND_INT4) wq[t][d + h][0] = *reinterpret_cast<const uint4*>(&v);
+          else wq[t][d][h] = *reinterpret_cast<const uint4*>(&v);
+        }
       }
     }
   }
   // value of group e (0-based in the slice) from those words: for 16-bit scales the first
-  // group sits in the high half of word 0 when soff is odd
-  const bool odd = esz == 2 && (soff & 1);
+  // group sits in the high half of word 0 when soff is odd (the same for every row tile:
+  // their offsets differ by 16 rows of ngroups words)
+  const bool odd = esz == 2 && (soff[0] & 1);
   auto group_value = [&](const uint32_t* wds, int e) -> float {
     if constexpr (SD == MIQ_F32) {
       return __builtin_bit_cast(float, wds[e]);
@@ -191,8 +227,9 @@ wo_tile_kernel(TileParams p) {
   // unpack order), then xsum [steps][16] fp32, the sum of each row over each k-step times
   // the code bias kXBias (the MFMA sees codes as 128 + u; symmetric int4 weights are u - 8)
   constexpr float kXBias = KIND == KIND_INT4 && !HZ ? -136.f : -128.f;
-  const int xstride = p.steps * kStepK + 8;
+  const int xstride = p.xsteps * kStepK + 8;
   float* xsum = reinterpret_cast<float*>(lds + M * xstride);
+  const int kbc = kb * (kStepK / 8);  // the first 16-byte column staged
   for (int base = 0; base < npieces; base += XP * 64) {
     if (base != 0) load_x(base);
 #pragma unroll
@@ -201,14 +238,14 @@ wo_tile_kernel(TileParams p) {
       const int i = base + lane + j * 64;
       const int ic = min(i, npieces - 1);
       const int m = ic / scols, c = st0 * (kStepK / 8) + ic - m * scols;
-      *reinterpret_cast<uint4*>(lds + m * xstride + c * 8) = KIND == KIND_INT4 ? permute_for_u4(xr[j]) : xr[j];
+      *reinterpret_cast<uint4*>(lds + m * xstride + (c - kbc) * 8) = KIND == KIND_INT4 ? permute_for_u4(xr[j]) : xr[j];
       // 16 consecutive lanes (one DPP row) hold the 16 pieces of one k-step of one row
       float sm = sum8_bf16(xr[j]);
       sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x111, 0xf, 0xf, true));
       sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x112, 0xf, 0xf, true));
       sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x114, 0xf, 0xf, true));
       sm += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, sm), 0x118, 0xf, 0xf, true));
-      if (i < npieces && (c & 15) == 15) xsum[(c >> 4) * 16 + m] = sm * kXBias;
+      if (i < npieces && (c & 15) == 15) xsum[((c - kbc) >> 4) * 16 + m] = sm * kXBias;
     }
   }
   // this wavefront's LDS writes are complete before its lanes read each other's
@@ -218,16 +255,19 @@ wo_tile_kernel(TileParams p) {
   MIQ_TRACE(2);
 
   // ---- multiply the slice. Per quantization group, T = sum_k x (128 + u) + kXBias * sum_k x
-  // (two MFMA chains and the staged sums), and acc += s * T (+ z * sum_k x with zero points)
+  // (two MFMA chains and the staged sums), and acc += s * T (+ z * sum_k x with zero points);
+  // the row tiles share the activation fragments
   const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-  f32x4 acc = z4, accg = z4, acc2 = z4, xsg = z4;
+  f32x4 acc[NT], accg[NT], acc2[NT], xsg = z4;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) acc[t] = accg[t] = acc2[t] = z4;
   int c_grp = 0, c_left = p.group_steps;
   const uint16_t* xrow = lds + min(r, M - 1) * xstride;
-  uint4 wnext;
+  uint4 wnext[NT];
 #pragma unroll
   for (int d = 0; d < NS; ++d) {
     if (d < nst) {
-      const int kl = st0 + d;
+      const int kl = st0 + d - kb;  // k-step within the staged range
       bf16x8 av[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -235,87 +275,111 @@ wo_tile_kernel(TileParams p) {
         av[j] = as_bf16x8(v.x, v.y, v.z, v.w);
       }
       const f32x4 xb = *reinterpret_cast<const f32x4*>(xsum + kl * 16 + g * 4);
-      uint4 wl[2];
-      if (KIND == KIND_INT8) {
-        lanes_to_mfma(bp_addr, wq[d][0], wq[d][1], wl[0], wl[1]);
-      } else if ((d & 1) == 0) {
-        lanes_to_mfma(bp_addr, wq[d][0], wq[d + 1][0], wl[0], wnext);
-      } else {
-        wl[0] = wnext;
+      if (!(KIND == KIND_INT4 && G1)) xsg += xb;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        uint4 wl[2];
+        if (KIND == KIND_INT8) {
+          lanes_to_mfma(bp_addr, wq[t][d][0], wq[t][d][1], wl[0], wl[1]);
+        } else if ((d & 1) == 0) {
+          lanes_to_mfma(bp_addr, wq[t][d][0], wq[t][d + 1][0], wl[0], wnext[t]);
+        } else {
+          wl[0] = wnext[t];
+        }
+        bf16x8 bv[4];
+        unpack_b<KIND>(wl, bv);
+        if (KIND == KIND_INT4 && G1) {
+          // one-step groups: the first chain starts from the step's bias, the second from
+          // zero, and the group ends here (scale and zero of group d: compile-time indices)
+          accg[t] = mfma(av[0], bv[0], xb);
+          acc2[t] = mfma(av[1], bv[1], z4);
+          accg[t] = mfma(av[2], bv[2], accg[t]);
+          acc2[t] = mfma(av[3], bv[3], acc2[t]);
+          const float sc = group_value(sw[t], d);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(sc, accg[t][v] + acc2[t][v], acc[t][v]);
+          if (HZ) {
+            const float zq = group_value(zw[t], d) * (1.f / kXBias);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(zq, xb[v], acc[t][v]);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            f32x4& chain = (j & 1) ? acc2[t] : (KIND == KIND_INT4 ? accg[t] : acc[t]);
+            chain = mfma(av[j], bv[j], chain);
+          }
+        }
       }
-      bf16x8 bv[4];
-      unpack_b<KIND>(wl, bv);
-      if (KIND == KIND_INT4 && G1) {
-        // one-step groups: the first chain starts from the step's bias, the second from
-        // zero, and the group ends here (scale and zero of group d: compile-time indices)
-        accg = mfma(av[0], bv[0], xb);
-        acc2 = mfma(av[1], bv[1], z4);
-        accg = mfma(av[2], bv[2], accg);
-        acc2 = mfma(av[3], bv[3], acc2);
-        const float sc = group_value(sw, d);
+      if (KIND == KIND_INT4 && !G1 && --c_left == 0) {  // end of a quantization group
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(sc, accg[v] + acc2[v], acc[v]);
-        if (HZ) {
-          const float zq = group_value(zw, d) * (1.f / kXBias);
-#pragma unroll
-          for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(zq, xb[v], acc[v]);
-        }
-      } else {
-        xsg += xb;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          f32x4& chain = (j & 1) ? acc2 : (KIND == KIND_INT4 ? accg : acc);
-          chain = mfma(av[j], bv[j], chain);
-        }
-        if (KIND == KIND_INT4 && --c_left == 0) {  // end of a quantization group
+        for (int t = 0; t < NT; ++t) {
           // group c_grp picked by a select chain (a run-time index into the word array
           // would spill it)
-          float sc = group_value(sw, 0), zv = 0.f;
-          if (HZ) zv = group_value(zw, 0);
+          float sc = group_value(sw[t], 0), zv = 0.f;
+          if (HZ) zv = group_value(zw[t], 0);
 #pragma unroll
           for (int e = 1; e < NS; ++e) {
             if (e > d) break;
-            sc = c_grp == e ? group_value(sw, e) : sc;
-            if (HZ) zv = c_grp == e ? group_value(zw, e) : zv;
+            sc = c_grp == e ? group_value(sw[t], e) : sc;
+            if (HZ) zv = c_grp == e ? group_value(zw[t], e) : zv;
           }
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(sc, accg[v] + acc2[v] + xsg[v], acc[v]);
+          for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(sc, accg[t][v] + acc2[t][v] + xsg[v], acc[t][v]);
           if (HZ) {
             const float zq = zv * (1.f / kXBias);
 #pragma unroll
-            for (int v = 0; v < 4; ++v) acc[v] = __builtin_fmaf(zq, xsg[v], acc[v]);
+            for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(zq, xsg[v], acc[t][v]);
           }
-          accg = z4;
-          acc2 = z4;
-          xsg = z4;
-          ++c_grp;
-          c_left = p.group_steps;
+          accg[t] = z4;
+          acc2[t] = z4;
         }
+        xsg = z4;
+        ++c_grp;
+        c_left = p.group_steps;
       }
     }
   }
   if (KIND == KIND_INT8) {
 #pragma unroll
-    for (int v = 0; v < 4; ++v) acc[v] += acc2[v] + xsg[v];
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[t][v] += acc2[t][v] + xsg[v];
   }
 
   MIQ_TRACE(3);
-  // ---- add the W partial tiles in wavefront order: red [W][M][16] fp32 over the x area
+  // ---- add the W partial tiles in wavefront order: red [W][M][16 NT] fp32 over the x area
+  constexpr int kCols = 16 * NT;
   __syncthreads();  // every wavefront is done reading the activations
   float* red = reinterpret_cast<float*>(lds);
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int m = g * 4 + v;  // lane (r, g) holds y[4 g + v][n0 + r]
-    if (m < M) red[(wv * M + m) * 16 + r] = acc[v];
-  }
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = g * 4 + v;  // lane (r, g) holds y[4 g + v][n0 + 16 t + r]
+      if (m < M) red[(wv * M + m) * kCols + 16 * t + r] = acc[t][v];
+    }
   __syncthreads();
-  // kThreads >= 256 >= 16 M: one output per thread at most
-  for (int t = tid; t < M * 16; t += kThreads) {
-    const int m = t >> 4, n = n0 + (t & 15);
-    if ((t & 15) >= nrows) continue;
+  for (int t = tid; t < M * kCols; t += kThreads) {
+    const int m = t / kCols, col = t % kCols, n = n0 + col;
+    if ((col & 15) >= (col >= 16 ? nrows[NT - 1] : nrows[0])) continue;
     float o = 0.f;
 #pragma unroll
-    for (int w = 0; w < W; ++w) o += red[w * M * 16 + t];
+    for (int w = 0; w < W; ++w) o += red[w * M * kCols + t];
+    if (KS == 2) {
+      // the two halves of K meet in one word per output: each workgroup swaps in its sum,
+      // marked so that it is never the all-zero word (the bits of o with the sign flipped,
+      // -0 taken as +0). The first to arrive finds zero and is done; the second finds the
+      // other half, adds (a + b == b + a, so the result does not depend on the order of
+      // arrival), writes y and clears the word for the next call.
+      uint32_t bits = __builtin_bit_cast(uint32_t, o);
+      bits = bits == 0x80000000u ? 0u : bits;
+      uint32_t* word = p.pair + (int64_t)m * p.N + n;
+      const uint32_t other = __hip_atomic_exchange(word, bits ^ 0x80000000u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (other == 0u) continue;
+      o += __builtin_bit_cast(float, other ^ 0x80000000u);
+      __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     if (KIND == KIND_INT8)
       o = bf16_to_f32(f32_to_bf16(o)) * bf16_to_f32(f32_to_bf16(sd_to_f32<SD>(row_scale)));
     p.y[(int64_t)m * p.ldy + n] = f32_to_bf16(o);
@@ -323,50 +387,63 @@ wo_tile_kernel(TileParams p) {
   MIQ_TRACE(4);
 }
 
-template <int KIND, bool HZ, int SD, int W, bool G1>
+template <int KIND, bool HZ, int SD, int W, bool G1, int NT, int KS>
 void launch_tile_g(const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
   // the LDS limit is set once per kernel (thread-safe)
   static std::once_flag lds_once;
   std::call_once(lds_once, [&] {
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wo_tile_kernel<KIND, HZ, SD, W, G1>),
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&wo_tile_kernel<KIND, HZ, SD, W, G1, NT, KS>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, kTileLds);
   });
-  hipLaunchKernelGGL((wo_tile_kernel<KIND, HZ, SD, W, G1>), dim3(blocks), dim3(W * 64), lds, st, p);
+  hipLaunchKernelGGL((wo_tile_kernel<KIND, HZ, SD, W, G1, NT, KS>), dim3(blocks), dim3(W * 64), lds, st, p);
 }
 
-// int4 with one-step (128-code) groups has its own instantiation
+// int4 with one-step (128-code) groups has its own instantiation; int4 workgroups can hold
+// two row tiles over half of K each (shape = row tiles x halves of K: 1 or 4)
 template <int KIND, bool HZ, int SD, int W>
-void launch_tile(const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
-  if (KIND == KIND_INT4 && p.group_steps == 1) launch_tile_g<KIND, HZ, SD, W, true>(p, blocks, lds, st);
-  else launch_tile_g<KIND, HZ, SD, W, false>(p, blocks, lds, st);
+void launch_tile(int shape, const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
+  if constexpr (KIND == KIND_INT4) {
+    if (shape == 4) {  // two row tiles, two halves of K
+      if (p.group_steps == 1) launch_tile_g<KIND, HZ, SD, W, true, 2, 2>(p, blocks, lds, st);
+      else launch_tile_g<KIND, HZ, SD, W, false, 2, 2>(p, blocks, lds, st);
+      return;
+    }
+    if (p.group_steps == 1) {
+      launch_tile_g<KIND, HZ, SD, W, true, 1, 1>(p, blocks, lds, st);
+      return;
+    }
+  }
+  launch_tile_g<KIND, HZ, SD, W, false, 1, 1>(p, blocks, lds, st);
 }
 
 template <int KIND, bool HZ, int SD>
-void launch_w(int W, const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
-  if (W == 4) launch_tile<KIND, HZ, SD, 4>(p, blocks, lds, st);
-  else if (W == 8) launch_tile<KIND, HZ, SD, 8>(p, blocks, lds, st);
-  else launch_tile<KIND, HZ, SD, 16>(p, blocks, lds, st);
+void launch_w(int W, int shape, const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
+  if (W == 4) launch_tile<KIND, HZ, SD, 4>(shape, p, blocks, lds, st);
+  else if (W == 8) launch_tile<KIND, HZ, SD, 8>(shape, p, blocks, lds, st);
+  else launch_tile<KIND, HZ, SD, 16>(shape, p, blocks, lds, st);
 }
 
 template <int KIND, bool HZ>
-void launch_tile_sd(int sd, int W, const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
-  if (sd == MIQ_BF16) launch_w<KIND, HZ, MIQ_BF16>(W, p, blocks, lds, st);
-  else if (sd == MIQ_F16) launch_w<KIND, HZ, MIQ_F16>(W, p, blocks, lds, st);
-  else launch_w<KIND, HZ, MIQ_F32>(W, p, blocks, lds, st);
+void launch_tile_sd(int sd, int W, int shape, const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
+  if (sd == MIQ_BF16) launch_w<KIND, HZ, MIQ_BF16>(W, shape, p, blocks, lds, st);
+  else if (sd == MIQ_F16) launch_w<KIND, HZ, MIQ_F16>(W, shape, p, blocks, lds, st);
+  else launch_w<KIND, HZ, MIQ_F32>(W, shape, p, blocks, lds, st);
 }
 
 }  // namespace
 
 // The tile plan for (M, N, K): wavefronts per workgroup W (0 = the tile kernel does not
 // apply: more than 16 rows, a slice longer than 8 k-steps, or activations too large for
-// LDS), the unit of K slicing and the LDS bytes.
+// LDS), the unit of K slicing, row tiles per workgroup (nt = 2: two 16-row tiles over
+// half of K each, a pair of workgroups per 32 rows), the staged k-steps and the LDS bytes.
 struct TilePlan {
-  int W, units, unit_steps, rows;
+  int W, units, unit_steps, rows, nt, ks, xsteps;
   size_t lds_bytes;
+  unsigned blocks;
 };
 
-static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_steps) {
-  TilePlan pl{0, 0, 0, 0, 0};
+static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_steps, bool pair_ok) {
+  TilePlan pl{};
   if (M < 1 || M > 16 || N < 1 || K < kStepK) return pl;
   if (tuning().wo_stream) return pl;  // force the streamed kernel (tuning, tests)
   // int8 with more than 4 rows: the streamed kernel (N = 19456, K = 2560 on MI355X: tile
@@ -379,39 +456,61 @@ static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_s
   if (kind == KIND_INT4 && us % 2 == 1 && steps % (2 * us) == 0) us *= 2;
   const int64_t units = steps / us;
   if (us > kTileNS) return pl;
-  const int64_t xbytes = M * (steps * kStepK + 8) * 2;
+  // int4 from pair_min_m rows on: 32-row workgroups over half of K each. Every CU then
+  // stages half the activations of the one-tile plan (at M = 8 those are twice a tile's
+  // weight bytes and bound the launch), and the halves meet in one exchange word per
+  // output (which needs the caller's workspace)
+  const bool forced = tuning().wo_pair_min_m > 0;  // MIQ_WO_PAIR_MIN_M: from that M up to 16
+  const bool pair_m = forced ? M >= tuning().wo_pair_min_m : (M >= kPairMinM && M <= kPairMaxM);
+  const int ks = kind == KIND_INT4 && pair_ok && units >= 2 && pair_m && tuning().wo_pair_min_m >= 0 ? 2 : 1;
+  // (two row tiles per workgroup: 16-row pairs, 320 workgroups, measured 11.1 against
+  // 9.6 us at M = 8)
+  const int nt = ks;
+  const int64_t xsteps = (units + ks - 1) / ks * us;  // k-steps staged per workgroup
+  const int64_t xbytes = M * (xsteps * kStepK + 8) * 2;
   // rows per tile: 16 (MIQ_WO_ROWS overrides, tuning). With per-wavefront activation
   // staging, 16-row tiles measured faster than fewer rows spread over every CU (INT4
   // N = 2560, K = 9728 on MI355X: M = 1 6.5 against 6.7 us with 10-row tiles, M = 8 10.7
   // against 11.1 us); before that change the 10-row tiles had been 4 % faster at M = 1.
   int rows = 16;
-  if (tuning().wo_rows > 0) rows = std::max(1, std::min(16, tuning().wo_rows));
-  const int64_t tiles = (N + rows - 1) / rows;
+  if (ks == 1 && tuning().wo_rows > 0) rows = std::max(1, std::min(16, tuning().wo_rows));
+  const int64_t blocks = ks * ((N + rows * nt - 1) / (rows * nt));
+  const int64_t wunits = (units + ks - 1) / ks;  // units per workgroup, at most
   for (int W : {4, 8, 16}) {
-    if ((units + W - 1) / W * us > kTileNS) continue;
-    const size_t lds = (size_t)std::max<int64_t>(xbytes, (int64_t)W * M * 16 * 4) + (size_t)steps * 16 * 4;
+    if ((wunits + W - 1) / W * us > kTileNS) continue;
+    const size_t lds = (size_t)std::max<int64_t>(xbytes, (int64_t)W * M * 16 * nt * 4) + (size_t)xsteps * 16 * 4;
     if (lds > (size_t)kTileLds) return pl;
     // every tile should be resident at once (a second wave of workgroups would stage the
     // activations again): workgroups per CU from LDS and from 16 wavefronts per CU
     const int64_t per_cu = std::min<int64_t>((int64_t)kTileLds / (int64_t)lds, 16 / W);
-    if (tiles > per_cu * kCUs * 5 / 4) return pl;
+    if (blocks > per_cu * kCUs * 5 / 4) return pl;
     pl.W = W;
     pl.units = (int)units;
     pl.unit_steps = us;
     pl.lds_bytes = lds;
     pl.rows = rows;
+    pl.nt = nt;
+    pl.ks = ks;
+    pl.xsteps = (int)xsteps;
+    pl.blocks = (unsigned)blocks;
     return pl;
   }
   return pl;
 }
 
+// Bytes of exchange words the two-half int4 plan needs: one fp32 word per output.
+size_t wo_tile_pair_bytes(int64_t M, int64_t N) { return M >= 1 && M <= 16 ? (size_t)(M * N * 4) : 0; }
+
 // Launches the tile kernel when it applies (`launched` says whether it did); returns a
-// MIQ_* status.
+// MIQ_* status. `pair` / `pair_bytes`: zeroed exchange words from the caller's workspace
+// (may be null; the two-half plan then does not apply).
 int wo_tile_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, const void* scale,
                    const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int M,
-                   int N, int K, hipStream_t st, const char* name, bool& launched) {
+                   int N, int K, void* pair, size_t pair_bytes, hipStream_t st, const char* name, bool& launched) {
   launched = false;
-  const TilePlan pl = plan_tile(kind, M, N, K, group_steps);
+  const bool pair_ok = pair != nullptr && pair_bytes >= wo_tile_pair_bytes(M, N) &&
+                       (reinterpret_cast<uintptr_t>(pair) & 3) == 0;
+  const TilePlan pl = plan_tile(kind, M, N, K, group_steps, pair_ok);
   if (pl.W == 0) return MIQ_OK;
   MIQ_REQUIRE((int64_t)N * ldw < 0x7fff0000LL, "%s: weights of %lld bytes exceed 2 GiB", name, (long long)N * ldw);
   TileParams p{};
@@ -431,13 +530,14 @@ int wo_tile_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, i
   p.units = pl.units;
   p.unit_steps = pl.unit_steps;
   p.rows = pl.rows;
+  p.xsteps = pl.xsteps;
+  p.pair = pl.ks == 2 ? static_cast<uint32_t*>(pair) : nullptr;
   p.wbytes = (int)((int64_t)N * ldw);
   const int esz = sd == MIQ_F32 ? 4 : 2;
   p.sbytes = kind == KIND_INT4 ? (int)(((int64_t)N * ngroups * esz + 3) & ~3LL) : 0;
-  const unsigned blocks = (unsigned)((N + pl.rows - 1) / pl.rows);
-  if (kind == KIND_INT8) launch_tile_sd<KIND_INT8, false>(sd, pl.W, p, blocks, pl.lds_bytes, st);
-  else if (zero) launch_tile_sd<KIND_INT4, true>(sd, pl.W, p, blocks, pl.lds_bytes, st);
-  else launch_tile_sd<KIND_INT4, false>(sd, pl.W, p, blocks, pl.lds_bytes, st);
+  if (kind == KIND_INT8) launch_tile_sd<KIND_INT8, false>(sd, pl.W, 1, p, pl.blocks, pl.lds_bytes, st);
+  else if (zero) launch_tile_sd<KIND_INT4, true>(sd, pl.W, pl.nt * pl.ks, p, pl.blocks, pl.lds_bytes, st);
+  else launch_tile_sd<KIND_INT4, false>(sd, pl.W, pl.nt * pl.ks, p, pl.blocks, pl.lds_bytes, st);
   launched = true;
   return check_launch(name);
 }

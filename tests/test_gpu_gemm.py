@@ -145,14 +145,20 @@ def test_w4a16_scale_dtypes(sdt):
 # streamed split-K kernel (forced with MIQ_WO_STREAM) must give the same results there.
 # Cases: multi-wavefront slices (K = 9728), an odd number of k-steps (K = 1152), groups of
 # 3 k-steps, long groups, f32 scales.
+# The two-half plan (32-row workgroups over half of K, from 2 rows on by default) adds: 16
+# rows at the configuration's K (the largest LDS staging), N an odd number of 16-row tiles
+# (the last pair holds one tile), 3 units of K (halves of 1 and 2 units).
 TILE_CASES = [(1, 320, 9728, 128), (4, 320, 9728, 128), (3, 160, 1152, 128), (2, 96, 1152, 384),
               (8, 64, 4096, 512), (16, 64, 1024, 128), (7, 48, 2560, 256), (1, 2560, 9728, 128),
-              (5, 3008, 2048, 128)]
+              (5, 3008, 2048, 128), (16, 2560, 9728, 128), (8, 2576, 9728, 128), (12, 48, 9728, 128)]
 # kernel choice: the default plan (INT4: the panel kernel), the plan without the panel
-# kernel, the streamed kernel, and the tile kernel with a forced number of weight rows per
-# tile (16, and 7: a tile whose 128-byte loads are partly empty)
+# kernel, the streamed kernel, the tile kernel with a forced number of weight rows per
+# tile (16, and 7: a tile whose 128-byte loads are partly empty) on one workgroup per tile,
+# and the two-half plan forced from one row on
 KERNELS = {"auto": {}, "nopanel": {"MIQ_WO_PANEL": "0"}, "stream": {"MIQ_WO_STREAM": "1"},
-           "rows16": {"MIQ_WO_ROWS": "16", "MIQ_WO_PANEL": "0"}, "rows7": {"MIQ_WO_ROWS": "7", "MIQ_WO_PANEL": "0"}}
+           "rows16": {"MIQ_WO_ROWS": "16", "MIQ_WO_PANEL": "0", "MIQ_WO_PAIR_MIN_M": "-1"},
+           "rows7": {"MIQ_WO_ROWS": "7", "MIQ_WO_PANEL": "0", "MIQ_WO_PAIR_MIN_M": "-1"},
+           "pair": {"MIQ_WO_PANEL": "0", "MIQ_WO_PAIR_MIN_M": "1"}}
 
 
 @pytest.mark.parametrize("kernel", list(KERNELS))
@@ -192,17 +198,18 @@ def test_w8a16_tile_and_stream(kernel, M, N, K, miq_env):
 
 
 def test_split_k_repeated_calls_are_identical():
-    """The split-K counters are left at zero: back-to-back calls give identical bytes."""
+    """The split-K counters and the two-half plan's exchange words are left at zero:
+    back-to-back calls give identical bytes."""
     from kernels import quant_ops as ops
     case("w4a16 repeated split-K calls")
     w = make_w(2560, 9728, 30)
     q = O.int4_quantize(w, 128)
     qd = {k: v.to(DEV) for k, v in q.items()}
     outs = []
-    for M in (1, 8, 64, 1, 8, 64, 33, 33):
+    for M in (1, 8, 64, 16, 1, 8, 64, 16, 33, 33):
         x = make_x(M, 9728, 31).to(DEV)
         outs.append(ops.w4a16_linear(x, qd["qweight"], qd["scale"], qd["zero"]).cpu())
-    assert all(torch.equal(outs[i], outs[i + 3]) for i in range(3)) and torch.equal(outs[6], outs[7])
+    assert all(torch.equal(outs[i], outs[i + 4]) for i in range(4)) and torch.equal(outs[8], outs[9])
 
 
 @pytest.mark.parametrize("name", ["int8_wo", "int4_wo", "fp8"])

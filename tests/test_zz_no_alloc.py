@@ -44,10 +44,11 @@ def with_workspace(x, q):
 
 def test_noalloc_matches_workspace_entry_point():
     # (M, N, K, group, symmetric): the panel kernel with its largest scratch at config 2, the
-    # prefill kernel with a K split (200 rows: 80 tiles), a smaller panel launch, a
-    # tile-kernel launch (no scratch), then the first shape again
+    # prefill kernel with a K split (200 rows: 80 tiles), a smaller panel launch, two
+    # tile-kernel launches of the two-half plan (exchange words in the scratch), then the
+    # first shape again
     shapes = [(64, 2560, 9728, 128, True), (200, 2560, 9728, 128, False), (40, 1280, 4096, 256, False),
-              (8, 512, 1024, 128, False), (64, 2560, 9728, 128, True)]
+              (16, 2560, 9728, 128, True), (8, 512, 1024, 128, False), (64, 2560, 9728, 128, True)]
     for i, (M, N, K, group, sym) in enumerate(shapes):
         case(f"noalloc call {i}: M={M} N={N} K={K} g={group} sym={sym}")
         x, q = operands(M, N, K, group, sym, seed=70 + (i % 3))
