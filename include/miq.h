@@ -240,6 +240,29 @@ int miq_fp8_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, 
                 const int32_t* expert_ids, const int32_t* num_padded, void* workspace,
                 size_t workspace_bytes, void* out, void* stream);
 
+/* The three layers above with the routing taken straight from topk_ids ([T, k] int32 or
+ * int64, idx_dtype; the reference's fused_moe call takes topk_ids and aligns them itself,
+ * kernels/fused_moe/fused_moe_triton.py:110-121, moe_align.cu:5-88). Up to 1024 pairs and
+ * 256 experts (and, for int4, H a multiple of 128 and I of 64) the expert GEMMs form
+ * moe_align's layout in LDS and no align launch runs; otherwise miq_moe_align runs into the
+ * workspace. Same results as miq_moe_align followed by the layer above; same workspace
+ * size (miq_moe_workspace_bytes). */
+int miq_w4a16_moe_routed(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
+                         const uint8_t* gu_q, const void* gu_scale, const void* gu_zero,
+                         const uint8_t* dn_q, const void* dn_scale, const void* dn_zero,
+                         int sz_dtype, int64_t group, const void* topk_weights, int w_dtype,
+                         const void* topk_ids, int idx_dtype, void* workspace, size_t workspace_bytes,
+                         void* out, void* stream);
+int miq_w8a16_moe_routed(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
+                         const int8_t* gu_q, const void* gu_scale, const int8_t* dn_q, const void* dn_scale,
+                         int scale_dtype, const void* topk_weights, int w_dtype,
+                         const void* topk_ids, int idx_dtype, void* workspace, size_t workspace_bytes,
+                         void* out, void* stream);
+int miq_fp8_moe_routed(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
+                       const uint8_t* gu_q, const float* gu_scale, const uint8_t* dn_q, const float* dn_scale,
+                       const void* topk_weights, int w_dtype, const void* topk_ids, int idx_dtype,
+                       void* workspace, size_t workspace_bytes, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,7 @@ Tuning read_tuning() {
   const char* ml = getenv("MIQ_MOE_LDS_SCALES");
   t.moe_no_lds_scales = ml && atoi(ml) == 0;
   t.moe_align_scan = flag("MIQ_MOE_ALIGN_SCAN");
+  t.moe_align_launch = flag("MIQ_MOE_ALIGN_LAUNCH");
   return t;
 }
 

@@ -205,6 +205,7 @@ struct Tuning {
   bool moe_four_waves;        // MIQ_MOE_WAVES=4: four-wavefront streaming expert workgroups
   bool moe_no_lds_scales;     // MIQ_MOE_LDS_SCALES=0: per-k-step scale loads instead of LDS
   bool moe_align_scan;        // MIQ_MOE_ALIGN_SCAN: the one-wavefront-per-expert align
+  bool moe_align_launch;      // MIQ_MOE_ALIGN_LAUNCH: routed MoE entry points run moe_align
 };
 const Tuning& tuning();
 

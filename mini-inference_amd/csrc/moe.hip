@@ -206,6 +206,8 @@ struct MoeParams {
   const int32_t* sorted_ids;
   const int32_t* expert_ids;
   const int32_t* num_padded;
+  const void* topk_ids;  // routed launches: the expert GEMMs align the pairs themselves (else null)
+  int idx_dtype;
   uint16_t* hbuf;  // [max_padded, I] bf16: silu(gate) * up per sorted row
   uint16_t* ypair;  // [num_pairs, H] bf16: routed down-projection per pair (bf16-rounded values)
   int32_t* rank;    // [num_pairs]: position of the pair in sorted_ids (pairs of a lower expert first)
@@ -364,6 +366,10 @@ enum { MOE_GU = 0, MOE_DN = 1 };
 // us with 2, 70.3-71.1 with 4, 74-75 with 6 and 77-78 with 8 (16 slower still); with
 // eight-wavefront workgroups and LDS scales 4 measured the same as 2
 constexpr int kMoeD = 2;
+// Routed launches (no moe_align): every workgroup of the expert GEMMs reads topk_ids into
+// LDS and forms the moe_align layout itself, for up to kRtPairs pairs and kRtExperts experts
+constexpr int kRtPairs = 1024, kRtExperts = 256;
+constexpr size_t kMoeStaticLds = 4096;  // the streaming kernel's static LDS, rounded up
 constexpr int kMoeChunk = 16;  // k-steps of activations staged at once
 // FP8 experts (e4m3fn codes, one fp32 scale per weight row), next to wo_core's INT8 / INT4;
 // their activation rows are staged whole (K <= kF8Steps k-steps: one byte per code, so twice
@@ -394,8 +400,14 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
   constexpr bool B1 = I8 || F8;  // one byte per code: a k-step of a tile is two line loads
   constexpr int NR = 2, NL = B1 ? 2 : 1, D = kMoeD;
   __shared__ float s_xs[kTile], s_xr[kTile];  // FP8: the activation rows' scales and their reciprocals
+  // routed launches: the experts of the pairs (out-of-range ids as E), the padded group
+  // offsets of the experts (moe_align's layout), and the current tile's pairs
+  __shared__ uint16_t s_ids[kRtPairs];
+  __shared__ int s_off[kRtExperts + 1];
+  __shared__ int s_pair[kTile];
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
+  const bool routed = p.topk_ids != nullptr;
   const int K = MODE == MOE_GU ? p.H : p.I;
   const int steps = K / kStepK;
   const int64_t ldw = B1 ? K : K / 2;
@@ -403,7 +415,42 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
   const int64_t ngroups = B1 ? 1 : steps / p.group_steps;
   const uint16_t* xbase = MODE == MOE_GU ? p.hidden : p.hbuf;
   const int ldx = K;
-  const int npad = *p.num_padded;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  int npad;
+  if (routed) {
+    // the moe_align layout from topk_ids: pairs grouped by expert, each group padded to a
+    // multiple of kTile, groups in expert order (counts with LDS atomics: the sums do not
+    // depend on the order)
+    for (int e = tid; e <= p.E; e += kThreads) s_off[e] = 0;
+    __syncthreads();
+    for (int i = tid; i < p.num_pairs; i += kThreads) {
+      int e = p.idx_dtype == MIQ_INT64 ? (int)static_cast<const int64_t*>(p.topk_ids)[i]
+                                       : static_cast<const int32_t*>(p.topk_ids)[i];
+      e = e < 0 || e >= p.E ? p.E : e;
+      s_ids[i] = (uint16_t)e;
+      if (e < p.E) atomicAdd(&s_off[e], 1);
+    }
+    __syncthreads();
+    if (wv == 0) {  // exclusive scan of the padded counts in place, 64 experts per round
+      int carry = 0;
+      for (int e0 = 0; e0 < p.E; e0 += 64) {
+        const int e = e0 + lane;
+        const int c = e < p.E ? (s_off[e] + kTile - 1) / kTile * kTile : 0;
+        int incl = c;
+        for (int o = 1; o < 64; o <<= 1) {
+          const int up = __shfl_up(incl, o, 64);
+          if (lane >= o) incl += up;
+        }
+        if (e < p.E) s_off[e] = carry + incl - c;
+        carry += __shfl(incl, 63, 64);
+      }
+      if (lane == 0) s_off[p.E] = carry;
+    }
+    __syncthreads();
+    npad = s_off[p.E];
+  } else {
+    npad = *p.num_padded;
+  }
   const int xstride = kMoeChunk * kStepK + 8;
   // FP8 stages only the codes (kTile rows at pitch kF8Row), with the per-(row, k-step)
   // maxima after them
@@ -439,7 +486,18 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
     if (tile * kTile >= npad) break;
     const bool stage = !(one_chunk && tile == staged_tile);
     staged_tile = tile;
-    const int e = p.expert_ids[tile];
+    int e;
+    if (routed) {  // the expert whose padded group holds row tile * kTile (< npad here)
+      int lo = 0, hi = p.E - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (s_off[mid + 1] <= tile * kTile) lo = mid + 1;
+        else hi = mid;
+      }
+      e = lo;
+    } else {
+      e = p.expert_ids[tile];
+    }
     // weight rows of this wavefront's two tiles (within the whole [E * rows] matrix)
     int row[NR];
     if (MODE == MOE_GU) {
@@ -496,8 +554,29 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
         zq[d][t] = HZ ? __builtin_amdgcn_raw_buffer_load_b32(zrs, so, 0, 0) : 0u;
       }
     };
-    if (stage && tid < kTile) {
+    if (stage && routed && wv == 0) {
+      // the tile's pairs: ranks j0 .. j0 + 15 among the pairs of expert e, in ascending
+      // pair order (one ballot per 64 pairs); rows past the group are padding
+      const int j0 = tile * kTile - s_off[e];
+      if (lane < kTile) {
+        s_pair[lane] = p.num_pairs;
+        s_src[lane] = -1;
+      }
+      int base = 0;
+      for (int c0 = 0; c0 < p.num_pairs && base < j0 + kTile; c0 += 64) {
+        const int i = c0 + lane;
+        const bool hit = i < p.num_pairs && s_ids[i] == e;
+        const uint64_t mask = __ballot(hit);
+        const int m = base + __popcll(mask & below) - j0;
+        if (hit && m >= 0 && m < kTile) {
+          s_pair[m] = i;
+          s_src[m] = MODE == MOE_GU ? i / p.topk : tile * kTile + m;
+        }
+        base += __popcll(mask);
+      }
+    } else if (stage && tid < kTile) {
       const int pair = p.sorted_ids[tile * kTile + tid];
+      s_pair[tid] = pair;
       s_src[tid] = pair < p.num_pairs ? (MODE == MOE_GU ? pair / p.topk : tile * kTile + tid) : -1;
     }
     // SL: this lane's 4 groups of each tile (loads past the row's groups return zeros)
@@ -521,6 +600,11 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
 #pragma unroll
     for (int d = 0; d < D; ++d) request(d, d);
     __syncthreads();  // s_src ready (and the previous item is done with LDS)
+    // down: the pairs of this lane's output rows, read now (before the staging barrier,
+    // after which wavefront 0 may already fill s_pair for the next item)
+    int lpair[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) lpair[v] = MODE == MOE_DN ? s_pair[g * 4 + v] : 0;
     if constexpr (SL) {
       // (only this wavefront reads its slice, in program order after these writes)
 #pragma unroll
@@ -791,7 +875,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int m = g * 4 + v;
-        const int pair = p.sorted_ids[tile * kTile + m];
+        const int pair = lpair[v];
         if (pair < p.num_pairs) {
           const float w = load_scalar(p.topk_w, p.w_dtype, pair);
           const int n0 = blk * (32 * NW) + wv * 32 + r;
@@ -829,7 +913,7 @@ void launch_stream_gemm(const MoeParams& p, int max_tiles, hipStream_t st) {
   const int per8 = MODE == MOE_GU ? 16 * 8 : 32 * 8;  // weight columns / rows of an 8-wavefront item
   const int nout = MODE == MOE_GU ? p.I : p.H;
   const bool w8 = !tuning().moe_four_waves && nout % per8 == 0 &&
-                  2 * (lds + (sl ? 8 * kMoeScaleLdsPerWave<HZ> : 0)) <= (size_t)160 * 1024;
+                  2 * (lds + (sl ? 8 * kMoeScaleLdsPerWave<HZ> : 0) + kMoeStaticLds) <= (size_t)160 * 1024;
   const int blocks = nout / (w8 ? per8 : per8 / 2);
   // about two workgroups per CU, never more than the runs of items that could exist
   // runs of two items per workgroup where there are enough items for two workgroups per CU
@@ -980,10 +1064,20 @@ extern "C" int miq_moe_align(const void* topk_ids, int idx_dtype, int64_t num_pa
   return check_launch("moe_align");
 }
 
+// Workspace: hbuf [max_padded, I] bf16 | ypair [T * topk, H] bf16 | rank [T * topk] int32 |
+// then, for the routed entry points when they run moe_align themselves, sorted_ids
+// [max_padded] | expert_ids [max tiles] | num_padded [1] (int32).
+namespace {
+size_t align_up(size_t v) { return (v + 255) / 256 * 256; }
+size_t moe_base_bytes(int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I) {
+  return align_up(max_padded_rows(T * topk, E) * (size_t)I * 2) + align_up((size_t)T * topk * H * 2) +
+         align_up((size_t)T * topk * 4);
+}
+}  // namespace
+
 extern "C" size_t miq_moe_workspace_bytes(int64_t T, int64_t topk, int64_t E, int64_t H, int64_t I) {
-  const size_t hb = max_padded_rows(T * topk, E) * (size_t)I * 2;
-  const size_t yb = (size_t)T * topk * H * 2;
-  return ((hb + 255) / 256) * 256 + ((yb + 255) / 256) * 256 + (size_t)T * topk * 4;
+  const size_t rows = max_padded_rows(T * topk, E);
+  return moe_base_bytes(T, topk, E, H, I) + align_up(rows * 4) + align_up((rows + kTile - 1) / kTile * 4) + 256;
 }
 
 namespace {
@@ -992,7 +1086,8 @@ int run_moe(int kind, const void* hidden, int64_t T, int64_t H, int64_t I, int64
             const uint8_t* gu_q, const void* gu_scale, const void* gu_zero, const uint8_t* dn_q,
             const void* dn_scale, const void* dn_zero, int sz_dtype, int64_t group, const void* topk_weights,
             int w_dtype, const int32_t* sorted_ids, const int32_t* expert_ids, const int32_t* num_padded,
-            void* workspace, size_t workspace_bytes, void* out, void* stream, const char* name) {
+            const void* topk_ids, int idx_dtype, void* workspace, size_t workspace_bytes, void* out, void* stream,
+            const char* name) {
   const bool f8 = kind == KIND_FP8;
   const bool i8 = kind == KIND_INT8 || f8;  // one byte per code, one scale per weight row
   MIQ_REQUIRE(sz_dtype == MIQ_F32 || sz_dtype == MIQ_BF16 || sz_dtype == MIQ_F16, "%s: bad scale dtype", name);
@@ -1034,17 +1129,39 @@ int run_moe(int kind, const void* hidden, int64_t T, int64_t H, int64_t I, int64
   p.group_steps = i8 ? 1 : (int)(group / kStepK);
   p.topk_w = topk_weights;
   p.w_dtype = w_dtype;
+  const size_t max_rows = max_padded_rows(T * topk, E);
+  hipStream_t st = (hipStream_t)stream;
+  if (topk_ids) {
+    // routed: the expert GEMMs form moe_align's layout themselves where the pairs and
+    // experts fit their LDS tables and the streaming kernels take the layer (int4: H a
+    // multiple of 128 and I of 64); otherwise moe_align runs into the workspace's tail
+    MIQ_REQUIRE(idx_dtype == MIQ_INT32 || idx_dtype == MIQ_INT64, "%s: topk_ids must be int32 or int64", name);
+    const bool stream_path = i8 || (H % 128 == 0 && I % 64 == 0 && !tuning().moe_tiled);
+    if (stream_path && T * topk <= kRtPairs && E <= kRtExperts && !tuning().moe_align_launch) {
+      p.topk_ids = topk_ids;
+      p.idx_dtype = idx_dtype;
+    } else {
+      char* tail = static_cast<char*>(workspace) + moe_base_bytes(T, topk, E, H, I);
+      int32_t* ws_sorted = reinterpret_cast<int32_t*>(tail);
+      int32_t* ws_experts = reinterpret_cast<int32_t*>(tail + align_up(max_rows * 4));
+      int32_t* ws_npad = reinterpret_cast<int32_t*>(tail + align_up(max_rows * 4) + align_up((max_rows + kTile - 1) / kTile * 4));
+      const int rc = miq_moe_align(topk_ids, idx_dtype, T * topk, E, kTile, ws_sorted, ws_experts, ws_npad, stream);
+      if (rc) return rc;
+      sorted_ids = ws_sorted;
+      expert_ids = ws_experts;
+      num_padded = ws_npad;
+    }
+  }
+  MIQ_REQUIRE(p.topk_ids || (sorted_ids && expert_ids && num_padded), "%s: no routing given", name);
   p.sorted_ids = sorted_ids;
   p.expert_ids = expert_ids;
   p.num_padded = num_padded;
-  const size_t max_rows = max_padded_rows(T * topk, E);
   const size_t hb = ((max_rows * I * 2 + 255) / 256) * 256;
   p.hbuf = static_cast<uint16_t*>(workspace);
   p.ypair = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + hb);
   p.rank = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + hb + (((size_t)T * topk * H * 2 + 255) / 256) * 256);
   p.out = static_cast<uint16_t*>(out);
   const unsigned tiles = (unsigned)((max_rows + kTile - 1) / kTile);
-  hipStream_t st = (hipStream_t)stream;
   if (f8) {
     launch_stream_experts_g<KIND_FP8, false, MIQ_F32, false>(p, (int)tiles, st);
   } else if (i8) {
@@ -1083,8 +1200,19 @@ extern "C" int miq_w4a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I
                              const int32_t* num_padded, void* workspace, size_t workspace_bytes,
                              void* out, void* stream) {
   return run_moe(KIND_INT4, hidden, T, H, I, E, topk, gu_q, gu_scale, gu_zero, dn_q, dn_scale, dn_zero, sz_dtype,
-                 group, topk_weights, w_dtype, sorted_ids, expert_ids, num_padded, workspace, workspace_bytes, out,
-                 stream, "w4a16_moe");
+                 group, topk_weights, w_dtype, sorted_ids, expert_ids, num_padded, nullptr, 0, workspace,
+                 workspace_bytes, out, stream, "w4a16_moe");
+}
+
+extern "C" int miq_w4a16_moe_routed(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
+                                    const uint8_t* gu_q, const void* gu_scale, const void* gu_zero,
+                                    const uint8_t* dn_q, const void* dn_scale, const void* dn_zero,
+                                    int sz_dtype, int64_t group, const void* topk_weights, int w_dtype,
+                                    const void* topk_ids, int idx_dtype, void* workspace, size_t workspace_bytes,
+                                    void* out, void* stream) {
+  return run_moe(KIND_INT4, hidden, T, H, I, E, topk, gu_q, gu_scale, gu_zero, dn_q, dn_scale, dn_zero, sz_dtype,
+                 group, topk_weights, w_dtype, nullptr, nullptr, nullptr, topk_ids, idx_dtype, workspace,
+                 workspace_bytes, out, stream, "w4a16_moe_routed");
 }
 
 extern "C" int miq_fp8_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
@@ -1093,8 +1221,17 @@ extern "C" int miq_fp8_moe(const void* hidden, int64_t T, int64_t H, int64_t I, 
                            const int32_t* expert_ids, const int32_t* num_padded, void* workspace,
                            size_t workspace_bytes, void* out, void* stream) {
   return run_moe(KIND_FP8, hidden, T, H, I, E, topk, gu_q, gu_scale, nullptr, dn_q, dn_scale, nullptr, MIQ_F32, 0,
-                 topk_weights, w_dtype, sorted_ids, expert_ids, num_padded, workspace, workspace_bytes, out, stream,
-                 "fp8_moe");
+                 topk_weights, w_dtype, sorted_ids, expert_ids, num_padded, nullptr, 0, workspace, workspace_bytes,
+                 out, stream, "fp8_moe");
+}
+
+extern "C" int miq_fp8_moe_routed(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
+                                  const uint8_t* gu_q, const float* gu_scale, const uint8_t* dn_q,
+                                  const float* dn_scale, const void* topk_weights, int w_dtype, const void* topk_ids,
+                                  int idx_dtype, void* workspace, size_t workspace_bytes, void* out, void* stream) {
+  return run_moe(KIND_FP8, hidden, T, H, I, E, topk, gu_q, gu_scale, nullptr, dn_q, dn_scale, nullptr, MIQ_F32, 0,
+                 topk_weights, w_dtype, nullptr, nullptr, nullptr, topk_ids, idx_dtype, workspace, workspace_bytes,
+                 out, stream, "fp8_moe_routed");
 }
 
 extern "C" int miq_w8a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
@@ -1105,5 +1242,16 @@ extern "C" int miq_w8a16_moe(const void* hidden, int64_t T, int64_t H, int64_t I
                              void* out, void* stream) {
   return run_moe(KIND_INT8, hidden, T, H, I, E, topk, reinterpret_cast<const uint8_t*>(gu_q), gu_scale, nullptr,
                  reinterpret_cast<const uint8_t*>(dn_q), dn_scale, nullptr, scale_dtype, 0, topk_weights, w_dtype,
-                 sorted_ids, expert_ids, num_padded, workspace, workspace_bytes, out, stream, "w8a16_moe");
+                 sorted_ids, expert_ids, num_padded, nullptr, 0, workspace, workspace_bytes, out, stream, "w8a16_moe");
+}
+
+extern "C" int miq_w8a16_moe_routed(const void* hidden, int64_t T, int64_t H, int64_t I, int64_t E, int64_t topk,
+                                    const int8_t* gu_q, const void* gu_scale, const int8_t* dn_q,
+                                    const void* dn_scale, int scale_dtype, const void* topk_weights, int w_dtype,
+                                    const void* topk_ids, int idx_dtype, void* workspace, size_t workspace_bytes,
+                                    void* out, void* stream) {
+  return run_moe(KIND_INT8, hidden, T, H, I, E, topk, reinterpret_cast<const uint8_t*>(gu_q), gu_scale, nullptr,
+                 reinterpret_cast<const uint8_t*>(dn_q), dn_scale, nullptr, scale_dtype, 0, topk_weights, w_dtype,
+                 nullptr, nullptr, nullptr, topk_ids, idx_dtype, workspace, workspace_bytes, out, stream,
+                 "w8a16_moe_routed");
 }

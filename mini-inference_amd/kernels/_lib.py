@@ -58,6 +58,12 @@ SIGNATURES = {
     "miq_fp8_moe": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I32, _P, _P, _P, _P, _SZ, _P, _P]),
     "miq_w4a16_moe": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I32, _I64, _P,
                              _I32, _P, _P, _P, _P, _SZ, _P, _P]),
+    "miq_w4a16_moe_routed": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _P, _I32, _I64, _P,
+                                    _I32, _P, _I32, _P, _SZ, _P, _P]),
+    "miq_w8a16_moe_routed": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I32, _P, _I32, _P, _I32,
+                                    _P, _SZ, _P, _P]),
+    "miq_fp8_moe_routed": (_I32, [_P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _P, _I32, _P, _I32, _P, _SZ,
+                                  _P, _P]),
 }
 
 _lib = None

@@ -393,3 +393,47 @@ def test_fused_moe_scale_dtypes(kind, sdt):
                              dn["qweight"].to(DEV), dn["scale"].to(DEV)).float().cpu()
         err = (got - loop).abs()
         assert (err <= 1e-2 + 2e-2 * loop.abs()).all(), err.max().item()
+
+
+@pytest.mark.parametrize("kind", ["int4", "int8", "fp8"])
+@pytest.mark.parametrize("T,H,I,E,k,pad", [(64, 2048, 1024, 64, 8, False), (5, 256, 128, 8, 2, True),
+                                           (33, 512, 256, 6, 3, True), (160, 256, 128, 64, 8, False),
+                                           (3, 256, 128, 300, 4, False), (128, 256, 128, 256, 8, True)])
+@pytest.mark.parametrize("ids_dtype", [torch.int64, torch.int32])
+def test_routed_layer_equals_align_then_layer(kind, T, H, I, E, k, pad, ids_dtype, miq_env):
+    """The routed entry points (the expert GEMMs align the pairs in LDS, no align launch)
+    give the same bytes as moe_align followed by the layer: 1024 pairs and 256 experts (the
+    LDS tables' limits, (128, .., 256, 8)) and beyond them (160 tokens of 8 slots, 300
+    experts: moe_align runs inside the call), with padding ids, and with the in-LDS path
+    switched off (MIQ_MOE_ALIGN_LAUNCH)."""
+    from kernels.fused_moe import fused_moe_fp8, fused_moe_int4, fused_moe_int8
+    case(f"routed {kind} moe T={T} H={H} I={I} E={E} k={k} pad={pad} ids {ids_dtype}")
+    g = torch.Generator().manual_seed(41)
+    wgu = (torch.randn(E, 2 * I, H, generator=g) * 0.02).to(torch.bfloat16)
+    wdn = (torch.randn(E, H, I, generator=g) * 0.02).to(torch.bfloat16)
+    hidden, w, idx = routed(T, H, E, k, seed=42)
+    idx = idx.clone()
+    if pad:
+        idx[::3, 0] = E
+        idx[1::7, :] = E
+    idx = idx.to(ids_dtype)
+    if kind == "int4":
+        gu, dn = O.int4_quantize(wgu, 128), O.int4_quantize(wdn, 128)
+        args = [gu["qweight"], gu["scale"], gu["zero"], dn["qweight"], dn["scale"], dn["zero"]]
+        fn = fused_moe_int4
+    elif kind == "int8":
+        gu, dn = O.int8_quantize(wgu), O.int8_quantize(wdn)
+        args = [gu["qweight"], gu["scale"], dn["qweight"], dn["scale"]]
+        fn = fused_moe_int8
+    else:
+        gu, dn = O.fp8_quantize(wgu), O.fp8_quantize(wdn)
+        args = [gu["qweight"], gu["scale"], dn["qweight"], dn["scale"]]
+        fn = fused_moe_fp8
+    dev_args = [hidden.to(DEV), idx.to(DEV), w.to(DEV)] + [a.to(DEV) for a in args]
+    want = fn(*dev_args, routed=False)
+    got = fn(*dev_args)
+    again = fn(*dev_args)
+    miq_env("MIQ_MOE_ALIGN_LAUNCH", "1")
+    launched = fn(*dev_args)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want) and torch.equal(again, want) and torch.equal(launched, want)
