@@ -369,6 +369,7 @@ constexpr int kMoeD = 2;
 // Routed launches (no moe_align): every workgroup of the expert GEMMs reads topk_ids into
 // LDS and forms the moe_align layout itself, for up to kRtPairs pairs and kRtExperts experts
 constexpr int kRtPairs = 1024, kRtExperts = 256;
+constexpr int kRtTiles = (kRtPairs + kRtExperts * (16 - 1) + 15) / 16;  // padded tiles at most
 constexpr size_t kMoeStaticLds = 4096;  // the streaming kernel's static LDS, rounded up
 constexpr int kMoeChunk = 16;  // k-steps of activations staged at once
 // FP8 experts (e4m3fn codes, one fp32 scale per weight row), next to wo_core's INT8 / INT4;
@@ -404,6 +405,8 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
   // offsets of the experts (moe_align's layout), and the current tile's pairs
   __shared__ uint16_t s_ids[kRtPairs];
   __shared__ int s_off[kRtExperts + 1];
+  __shared__ uint16_t s_te[kRtTiles];       // expert of each padded tile
+  __shared__ int s_cc[kRtPairs / 64];       // hits of the current expert per 64-pair chunk
   __shared__ int s_pair[kTile];
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, g = lane >> 4;
@@ -447,6 +450,9 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
       if (lane == 0) s_off[p.E] = carry;
     }
     __syncthreads();
+    for (int e = tid; e < p.E; e += kThreads)
+      for (int t = s_off[e] / kTile; t < s_off[e + 1] / kTile; ++t) s_te[t] = (uint16_t)e;
+    __syncthreads();
     npad = s_off[p.E];
   } else {
     npad = *p.num_padded;
@@ -486,18 +492,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
     if (tile * kTile >= npad) break;
     const bool stage = !(one_chunk && tile == staged_tile);
     staged_tile = tile;
-    int e;
-    if (routed) {  // the expert whose padded group holds row tile * kTile (< npad here)
-      int lo = 0, hi = p.E - 1;
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (s_off[mid + 1] <= tile * kTile) lo = mid + 1;
-        else hi = mid;
-      }
-      e = lo;
-    } else {
-      e = p.expert_ids[tile];
-    }
+    const int e = routed ? (int)s_te[tile] : p.expert_ids[tile];
     // weight rows of this wavefront's two tiles (within the whole [E * rows] matrix)
     int row[NR];
     if (MODE == MOE_GU) {
@@ -554,31 +549,6 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
         zq[d][t] = HZ ? __builtin_amdgcn_raw_buffer_load_b32(zrs, so, 0, 0) : 0u;
       }
     };
-    if (stage && routed && wv == 0) {
-      // the tile's pairs: ranks j0 .. j0 + 15 among the pairs of expert e, in ascending
-      // pair order (one ballot per 64 pairs); rows past the group are padding
-      const int j0 = tile * kTile - s_off[e];
-      if (lane < kTile) {
-        s_pair[lane] = p.num_pairs;
-        s_src[lane] = -1;
-      }
-      int base = 0;
-      for (int c0 = 0; c0 < p.num_pairs && base < j0 + kTile; c0 += 64) {
-        const int i = c0 + lane;
-        const bool hit = i < p.num_pairs && s_ids[i] == e;
-        const uint64_t mask = __ballot(hit);
-        const int m = base + __popcll(mask & below) - j0;
-        if (hit && m >= 0 && m < kTile) {
-          s_pair[m] = i;
-          s_src[m] = MODE == MOE_GU ? i / p.topk : tile * kTile + m;
-        }
-        base += __popcll(mask);
-      }
-    } else if (stage && tid < kTile) {
-      const int pair = p.sorted_ids[tile * kTile + tid];
-      s_pair[tid] = pair;
-      s_src[tid] = pair < p.num_pairs ? (MODE == MOE_GU ? pair / p.topk : tile * kTile + tid) : -1;
-    }
     // SL: this lane's 4 groups of each tile (loads past the row's groups return zeros)
     uint32_t scw[NR][2], zcw[NR][2];
     if constexpr (SL) {
@@ -599,6 +569,43 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
     }
 #pragma unroll
     for (int d = 0; d < D; ++d) request(d, d);
+    // the tile's pairs (after the weight requests, which do not depend on them)
+    if (stage && routed) {
+      // the tile's pairs: ranks j0 .. j0 + 15 among the pairs of expert e, in ascending
+      // pair order; rows past the group are padding. Wavefront w takes the 64-pair chunks
+      // w, w + NW, ..: a ballot counts the chunk's pairs of e, and after a barrier each
+      // chunk adds the counts of the chunks before it.
+      const int j0 = tile * kTile - s_off[e];
+      const int nch = (p.num_pairs + 63) >> 6;
+      uint64_t mk[kRtPairs / 64 / NW];
+#pragma unroll
+      for (int q = 0; q < kRtPairs / 64 / NW; ++q) {
+        const int c = wv + q * NW, i = c * 64 + lane;
+        mk[q] = __ballot(c < nch && i < p.num_pairs && s_ids[i] == e);
+        if (c < nch && lane == 0) s_cc[c] = __popcll(mk[q]);
+      }
+      if (tid < kTile) {
+        s_pair[tid] = p.num_pairs;
+        s_src[tid] = -1;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < kRtPairs / 64 / NW; ++q) {
+        const int c = wv + q * NW, i = c * 64 + lane;
+        if (c >= nch) break;  // uniform
+        int base = 0;
+        for (int b = 0; b < c; ++b) base += s_cc[b];
+        const int m = base + __popcll(mk[q] & below) - j0;
+        if (((mk[q] >> lane) & 1) && m >= 0 && m < kTile) {
+          s_pair[m] = i;
+          s_src[m] = MODE == MOE_GU ? i / p.topk : tile * kTile + m;
+        }
+      }
+    } else if (stage && tid < kTile) {
+      const int pair = p.sorted_ids[tile * kTile + tid];
+      s_pair[tid] = pair;
+      s_src[tid] = pair < p.num_pairs ? (MODE == MOE_GU ? pair / p.topk : tile * kTile + tid) : -1;
+    }
     __syncthreads();  // s_src ready (and the previous item is done with LDS)
     // down: the pairs of this lane's output rows, read now (before the staging barrier,
     // after which wavefront 0 may already fill s_pair for the next item)
