@@ -22,6 +22,8 @@ Tuning read_tuning() {
   t.wo_rows = rows ? atoi(rows) : 0;
   const char* pmin = getenv("MIQ_WO_PAIR_MIN_M");
   t.wo_pair_min_m = pmin ? atoi(pmin) : 0;
+  const char* t2 = getenv("MIQ_WO_INT8_TILE2_MIN_M");
+  t.wo_int8_tile2_min_m = t2 ? atoi(t2) : 0;
   t.wo_msplit_set = pair("MIQ_WO_MSPLIT", t.wo_msplit_nr, t.wo_msplit_s);
   t.wo_plan_set = pair("MIQ_WO_PLAN", t.wo_plan_nr, t.wo_plan_s);
   const char* panel = getenv("MIQ_WO_PANEL");

@@ -189,6 +189,8 @@ struct Tuning {
   int wo_rows;                // MIQ_WO_ROWS: rows per tile of the tile kernel (0: default)
   int wo_pair_min_m;          // MIQ_WO_PAIR_MIN_M: the tile kernel's two-half int4 plan from
                               // this M up to 16 (0: default range, -1: never)
+  int wo_int8_tile2_min_m;    // MIQ_WO_INT8_TILE2_MIN_M: int8 tile kernel with two row tiles per
+                              // workgroup from this M up to 16 (0: default range, -1: never)
   bool wo_msplit_set;         // MIQ_WO_MSPLIT="NR,S": M-split plan of the streamed kernel
   int wo_msplit_nr, wo_msplit_s;
   bool wo_plan_set;           // MIQ_WO_PLAN="NR,S": plan of the streamed kernel

@@ -62,6 +62,12 @@ constexpr int kCUs = 256;                  // MI355X compute units
 // 12.0 / 12.8 us against 7.6 / 8.7 / 9.5 / 10.25 / 11.3 / 12.3 / 13.9 us: the exchange costs
 // about 1 us and pays at 8 to 10 rows, where a CU's staged activations outweigh its weights
 constexpr int kPairMinM = 7, kPairMaxM = 10;
+// int8: rows of the plan with two row tiles per workgroup over all of K. INT8 N = 19456,
+// K = 2560 on MI355X (rotating weight copies), one tile per workgroup (M > 4: the streamed
+// kernel) against two: M = 1 / 4 / 5 / 6 / 8 / 12 took 10.9-11.4 / 13.3-13.4 / 14.7-15.0 /
+// 14.6-15.2 / 15.2-15.4 / 16.4-16.6 us against 12.3 / 13.1-13.2 / 13.6-13.9 / 14.9-15.0 /
+// 15.9-16.1 / 18.2-18.3 us
+constexpr int kInt8Tile2MinM = 4, kInt8Tile2MaxM = 5;
 // activation pieces (16 B) per lane per round (int8 holds twice the weight registers):
 // 12 x 64 pieces cover a wavefront's slice at M = 8 (8 rows x 6 k-steps) in one round;
 // 16 measured slower (register pressure)
@@ -93,8 +99,11 @@ struct TileParams {
 template <int KIND, bool HZ, int SD, int W, bool G1, int NT, int KS>
 __global__ void __launch_bounds__(W * 64)
 wo_tile_kernel(TileParams p) {
-  static_assert(KIND == KIND_INT4 || (NT == 1 && KS == 1), "int8 takes one row tile over all of K");
-  constexpr int kThreads = W * 64, NS = kTileNS, XP = tile_xp<KIND>();
+  static_assert(KIND == KIND_INT4 || KS == 1, "int8 workgroups cover all of K");
+  // k-steps in flight per wavefront: int8 with two row tiles holds 4 (the weight registers
+  // of 8 would leave one wavefront per SIMD)
+  constexpr int NS = KIND == KIND_INT8 && NT == 2 ? kTileNS / 2 : kTileNS;
+  constexpr int kThreads = W * 64, XP = tile_xp<KIND>();
   constexpr int kStepBytes = KIND == KIND_INT4 ? kStepK / 2 : kStepK;  // per weight row
   extern __shared__ __align__(16) uint16_t lds[];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -165,7 +174,7 @@ wo_tile_kernel(TileParams p) {
   // int8: the row scale of the output this thread writes at the end (thread t < 16 M
   // writes row n0 + t % 16), requested now rather than after the reduction
   uint32_t row_scale = 0;
-  if (KIND == KIND_INT8 && tid < M * 16) row_scale = load_sd_raw<SD>(p.scale, min(n0 + (tid & 15), p.N - 1));
+  if (KIND == KIND_INT8 && NT == 1 && tid < M * 16) row_scale = load_sd_raw<SD>(p.scale, min(n0 + (tid & 15), p.N - 1));
   // int4: the scale (and zero) words of the slice's groups, at most NS of them, with two
   // 16-byte loads from the aligned word holding the first one. They are requested before
   // the weights: the multiply of k-step d then waits only for the weight loads up to d
@@ -380,8 +389,10 @@ wo_tile_kernel(TileParams p) {
       o += __builtin_bit_cast(float, other ^ 0x80000000u);
       __hip_atomic_store(word, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (KIND == KIND_INT8)
-      o = bf16_to_f32(f32_to_bf16(o)) * bf16_to_f32(f32_to_bf16(sd_to_f32<SD>(row_scale)));
+    if (KIND == KIND_INT8) {
+      const uint32_t rs = NT == 1 ? row_scale : load_sd_raw<SD>(p.scale, n);
+      o = bf16_to_f32(f32_to_bf16(o)) * bf16_to_f32(f32_to_bf16(sd_to_f32<SD>(rs)));
+    }
     p.y[(int64_t)m * p.ldy + n] = f32_to_bf16(o);
   }
   MIQ_TRACE(4);
@@ -399,9 +410,16 @@ void launch_tile_g(const TileParams& p, unsigned blocks, size_t lds, hipStream_t
 }
 
 // int4 with one-step (128-code) groups has its own instantiation; int4 workgroups can hold
-// two row tiles over half of K each (shape = row tiles x halves of K: 1 or 4)
+// two row tiles over half of K each, int8 workgroups two row tiles over all of K (shape =
+// row tiles x halves of K: 1, 2 or 4)
 template <int KIND, bool HZ, int SD, int W>
 void launch_tile(int shape, const TileParams& p, unsigned blocks, size_t lds, hipStream_t st) {
+  if constexpr (KIND == KIND_INT8) {
+    if (shape == 2) {  // two row tiles over all of K
+      launch_tile_g<KIND, HZ, SD, W, false, 2, 1>(p, blocks, lds, st);
+      return;
+    }
+  }
   if constexpr (KIND == KIND_INT4) {
     if (shape == 4) {  // two row tiles, two halves of K
       if (p.group_steps == 1) launch_tile_g<KIND, HZ, SD, W, true, 2, 2>(p, blocks, lds, st);
@@ -449,7 +467,11 @@ static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_s
   // int8 with more than 4 rows: the streamed kernel (N = 19456, K = 2560 on MI355X: tile
   // kernel at M = 3 / 4 / 8 / 16 12.0 / 12.9 / 15.3 / 16.9 us, streamed 14.1 / 14.2 / 15.2 /
   // 17.0 us; the staged activations of a tile grow with M)
-  if (kind == KIND_INT8 && M > 4) return pl;
+  // int8 at 4 and 5 rows: workgroups of two 16-row tiles share one staging of the
+  // activations (half the staged bytes per weight byte)
+  const int t2 = tuning().wo_int8_tile2_min_m;  // MIQ_WO_INT8_TILE2_MIN_M: from that M up to 16
+  const bool int8_two = kind == KIND_INT8 && t2 >= 0 && (t2 > 0 ? M >= t2 : (M >= kInt8Tile2MinM && M <= kInt8Tile2MaxM));
+  if (kind == KIND_INT8 && M > 4 && !int8_two) return pl;
   const int64_t steps = K / kStepK;
   int us = kind == KIND_INT4 ? group_steps : 1;
   // int4 slices start on an even k-step when they can (whole 128-byte lines per load)
@@ -465,7 +487,8 @@ static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_s
   const int ks = kind == KIND_INT4 && pair_ok && units >= 2 && pair_m && tuning().wo_pair_min_m >= 0 ? 2 : 1;
   // (two row tiles per workgroup: 16-row pairs, 320 workgroups, measured 11.1 against
   // 9.6 us at M = 8)
-  const int nt = ks;
+  const int nt = int8_two ? 2 : ks;
+  const int ns = kind == KIND_INT8 && nt == 2 ? kTileNS / 2 : kTileNS;  // k-steps per wavefront at most
   const int64_t xsteps = (units + ks - 1) / ks * us;  // k-steps staged per workgroup
   const int64_t xbytes = M * (xsteps * kStepK + 8) * 2;
   // rows per tile: 16 (MIQ_WO_ROWS overrides, tuning). With per-wavefront activation
@@ -473,11 +496,11 @@ static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_s
   // N = 2560, K = 9728 on MI355X: M = 1 6.5 against 6.7 us with 10-row tiles, M = 8 10.7
   // against 11.1 us); before that change the 10-row tiles had been 4 % faster at M = 1.
   int rows = 16;
-  if (ks == 1 && tuning().wo_rows > 0) rows = std::max(1, std::min(16, tuning().wo_rows));
+  if (nt == 1 && tuning().wo_rows > 0) rows = std::max(1, std::min(16, tuning().wo_rows));
   const int64_t blocks = ks * ((N + rows * nt - 1) / (rows * nt));
   const int64_t wunits = (units + ks - 1) / ks;  // units per workgroup, at most
   for (int W : {4, 8, 16}) {
-    if ((wunits + W - 1) / W * us > kTileNS) continue;
+    if ((wunits + W - 1) / W * us > ns) continue;
     const size_t lds = (size_t)std::max<int64_t>(xbytes, (int64_t)W * M * 16 * nt * 4) + (size_t)xsteps * 16 * 4;
     if (lds > (size_t)kTileLds) return pl;
     // every tile should be resident at once (a second wave of workgroups would stage the
@@ -535,7 +558,7 @@ int wo_tile_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, i
   p.wbytes = (int)((int64_t)N * ldw);
   const int esz = sd == MIQ_F32 ? 4 : 2;
   p.sbytes = kind == KIND_INT4 ? (int)(((int64_t)N * ngroups * esz + 3) & ~3LL) : 0;
-  if (kind == KIND_INT8) launch_tile_sd<KIND_INT8, false>(sd, pl.W, 1, p, pl.blocks, pl.lds_bytes, st);
+  if (kind == KIND_INT8) launch_tile_sd<KIND_INT8, false>(sd, pl.W, pl.nt, p, pl.blocks, pl.lds_bytes, st);
   else if (zero) launch_tile_sd<KIND_INT4, true>(sd, pl.W, pl.nt * pl.ks, p, pl.blocks, pl.lds_bytes, st);
   else launch_tile_sd<KIND_INT4, false>(sd, pl.W, pl.nt * pl.ks, p, pl.blocks, pl.lds_bytes, st);
   launched = true;

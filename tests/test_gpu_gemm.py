@@ -181,13 +181,20 @@ def test_w4a16_tile_and_stream(kernel, M, N, K, group, sdt, symmetric, miq_env):
     within(y, want)
 
 
-@pytest.mark.parametrize("kernel", list(KERNELS))
+# int8 kernels: as above, plus workgroups of two row tiles over all of K (at 4 and 5 rows by
+# default, forced from one row): N an odd number of 16-row tiles (2512, 1008), K = 4096
+# (eight wavefronts of 4 k-steps, the most that plan holds)
+KERNELS8 = dict(KERNELS, tile2={"MIQ_WO_INT8_TILE2_MIN_M": "1"}, one_tile={"MIQ_WO_INT8_TILE2_MIN_M": "-1"})
+
+
+@pytest.mark.parametrize("kernel", list(KERNELS8))
 @pytest.mark.parametrize("M,N,K", [(1, 19456, 2560), (2, 4096, 2560), (3, 160, 1152), (4, 64, 9728), (1, 2512, 2560),
-                                   (8, 19456, 2560), (16, 1008, 2560), (13, 2512, 1152)])
+                                   (8, 19456, 2560), (16, 1008, 2560), (13, 2512, 1152), (5, 2512, 2560),
+                                   (4, 1008, 4096)])
 def test_w8a16_tile_and_stream(kernel, M, N, K, miq_env):
     from kernels import quant_ops as ops
     case(f"w8a16 {kernel} M={M} N={N} K={K}")
-    for k, v in KERNELS[kernel].items():
+    for k, v in KERNELS8[kernel].items():
         miq_env(k, v)
     w = make_w(N, K, 52)
     x = make_x(M, K, 53)
