@@ -41,6 +41,7 @@ Tuning read_tuning() {
   t.fp8_old = flag("MIQ_FP8_OLD");
   const char* fw = getenv("MIQ_FP8_WAVES");
   t.fp8_four_waves = fw && atoi(fw) == 4;
+  t.fp8_quant_rows_wg = flag("MIQ_FP8_QUANT_ROWS_WG");
   t.moe_tiled = flag("MIQ_MOE_TILED");
   const char* mw = getenv("MIQ_MOE_WAVES");
   t.moe_four_waves = mw && atoi(mw) == 4;

@@ -203,6 +203,7 @@ struct Tuning {
   int wo_prefill_s;           // MIQ_WO_PREFILL_S: K splits of the prefill kernel (0: planned)
   bool fp8_old;               // MIQ_FP8_OLD: the previous FP8 GEMM kernel family
   bool fp8_four_waves;        // MIQ_FP8_WAVES=4
+  bool fp8_quant_rows_wg;     // MIQ_FP8_QUANT_ROWS_WG: one workgroup per row in fp8_quantize_rows
   bool moe_tiled;             // MIQ_MOE_TILED: the tiled expert kernels
   bool moe_four_waves;        // MIQ_MOE_WAVES=4: four-wavefront streaming expert workgroups
   bool moe_no_lds_scales;     // MIQ_MOE_LDS_SCALES=0: per-k-step scale loads instead of LDS

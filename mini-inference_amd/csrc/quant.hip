@@ -112,6 +112,69 @@ __global__ void int4_dequantize_kernel(const uint8_t* __restrict__ q, const void
 }
 
 // ---------------------------------------------------------------- fp8 rows (fp8.py:32-46)
+// e4m3 codes of 8 bf16 values x / s (r = RN(1 / s)): the hardware e4m3 (OCP) conversion
+// rounds to nearest even like f32_to_fp8; the inputs are clamped to +-448 first, as the
+// reference does
+__device__ inline uint2 fp8_encode8(const uint4& p, float s, float r) {
+  const uint32_t d[4] = {p.x, p.y, p.z, p.w};
+  int o[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      v[2 * i] = fminf(fmaxf(div_by_recip(bf16_to_f32(d[2 * h + i] & 0xffff), s, r), -448.f), 448.f);
+      v[2 * i + 1] = fminf(fmaxf(div_by_recip(bf16_to_f32(d[2 * h + i] >> 16), s, r), -448.f), 448.f);
+    }
+    o[h] = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
+    o[h] = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], o[h], true);
+  }
+  return make_uint2((uint32_t)o[0], (uint32_t)o[1]);
+}
+
+__device__ inline float max_abs8(const uint4& p, float amax) {
+  const uint32_t d[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    amax = fmaxf(amax, fabsf(bf16_to_f32(d[i] & 0xffff)));
+    amax = fmaxf(amax, fabsf(bf16_to_f32(d[i] >> 16)));
+  }
+  return amax;
+}
+
+// bf16 rows of at most 64 * kWaveHeld pieces of 8 (K <= 4096), 16-byte aligned: one
+// wavefront per row, the row held in registers between the max and the encode, the max
+// reduced across the wavefront (no LDS, no barrier). The codes and the scale are those of
+// the workgroup-per-row kernel below (the same maximum and the same expressions).
+constexpr int kWaveHeld = 8;
+__global__ void __launch_bounds__(kRowThreads)
+fp8_quantize_rows_wave_kernel(const uint16_t* __restrict__ x, int64_t K, int64_t ldx, int64_t rows,
+                              uint8_t* __restrict__ q, float* __restrict__ scale) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * (kRowThreads / 64) + (threadIdx.x >> 6);
+  if (row >= rows) return;  // whole wavefronts
+  const uint4* xv = reinterpret_cast<const uint4*>(x + row * ldx);
+  const int npc = (int)(K / 8);
+  uint4 held[kWaveHeld];
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < kWaveHeld; ++j) {
+    const int c = lane + 64 * j;
+    held[j] = c < npc ? xv[c] : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < kWaveHeld; ++j) amax = max_abs8(held[j], amax);
+  amax = wave_max(amax);
+  const float s = fmaxf(amax, 1e-12f) / 448.0f, rs = 1.0f / s;
+  uint2* qv = reinterpret_cast<uint2*>(q + row * K);
+#pragma unroll
+  for (int j = 0; j < kWaveHeld; ++j) {
+    const int c = lane + 64 * j;
+    if (c < npc) qv[c] = fp8_encode8(held[j], s, rs);
+  }
+  if (lane == 0) scale[row] = s;
+}
+
 __global__ void __launch_bounds__(kRowThreads)
 fp8_quantize_rows_kernel(const void* __restrict__ x, int x_dtype, int64_t K, int64_t ldx,
                          uint8_t* __restrict__ q, float* __restrict__ scale) {
@@ -132,44 +195,18 @@ fp8_quantize_rows_kernel(const void* __restrict__ x, int x_dtype, int64_t K, int
       const int64_t c = threadIdx.x + (int64_t)j * blockDim.x;
       held[j] = c < npc ? xv[c] : make_uint4(0, 0, 0, 0);
     }
-    auto piece_max = [&](const uint4& p) {
-      const uint32_t d[4] = {p.x, p.y, p.z, p.w};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        amax = fmaxf(amax, fabsf(bf16_to_f32(d[i] & 0xffff)));
-        amax = fmaxf(amax, fabsf(bf16_to_f32(d[i] >> 16)));
-      }
-    };
-#pragma unroll
-    for (int j = 0; j < kHeld; ++j) piece_max(held[j]);
-    for (int64_t c = threadIdx.x + (int64_t)kHeld * blockDim.x; c < npc; c += blockDim.x) piece_max(xv[c]);
+    for (int j = 0; j < kHeld; ++j) amax = max_abs8(held[j], amax);
+    for (int64_t c = threadIdx.x + (int64_t)kHeld * blockDim.x; c < npc; c += blockDim.x) amax = max_abs8(xv[c], amax);
     amax = block_reduce_max(amax, red);
     const float s = fmaxf(amax, 1e-12f) / 448.0f, rs = 1.0f / s;
     uint2* qv = reinterpret_cast<uint2*>(q + row * K);
-    // the hardware e4m3 (OCP) conversion rounds to nearest even like f32_to_fp8; the
-    // inputs are clamped to +-448 first, as the reference does
-    auto convert = [&](const uint4& p, int64_t c) {
-      const uint32_t d[4] = {p.x, p.y, p.z, p.w};
-      int o[2];
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        float v[4];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          v[2 * i] = fminf(fmaxf(div_by_recip(bf16_to_f32(d[2 * h + i] & 0xffff), s, rs), -448.f), 448.f);
-          v[2 * i + 1] = fminf(fmaxf(div_by_recip(bf16_to_f32(d[2 * h + i] >> 16), s, rs), -448.f), 448.f);
-        }
-        o[h] = __builtin_amdgcn_cvt_pk_fp8_f32(v[0], v[1], 0, false);
-        o[h] = __builtin_amdgcn_cvt_pk_fp8_f32(v[2], v[3], o[h], true);
-      }
-      qv[c] = make_uint2((uint32_t)o[0], (uint32_t)o[1]);
-    };
 #pragma unroll
     for (int j = 0; j < kHeld; ++j) {
       const int64_t c = threadIdx.x + (int64_t)j * blockDim.x;
-      if (c < npc) convert(held[j], c);
+      if (c < npc) qv[c] = fp8_encode8(held[j], s, rs);
     }
-    for (int64_t c = threadIdx.x + (int64_t)kHeld * blockDim.x; c < npc; c += blockDim.x) convert(xv[c], c);
+    for (int64_t c = threadIdx.x + (int64_t)kHeld * blockDim.x; c < npc; c += blockDim.x) qv[c] = fp8_encode8(xv[c], s, rs);
     if (threadIdx.x == 0) scale[row] = s;
     return;
   }
@@ -298,6 +335,13 @@ extern "C" int miq_fp8_quantize_rows(const void* x, int x_dtype, int64_t rows, i
   MIQ_REQUIRE(K > 0 && ldx >= K && rows >= 0, "fp8_quantize_rows: bad shape");
   if (rows == 0) return MIQ_OK;
   MIQ_REQUIRE(rows <= 0x7fffffff, "fp8_quantize_rows: too many rows");
+  if (x_dtype == MIQ_BF16 && K % 8 == 0 && K <= 64 * 8 * kWaveHeld && ldx % 8 == 0 &&
+      (reinterpret_cast<uintptr_t>(x) & 15) == 0 && !tuning().fp8_quant_rows_wg) {
+    const int64_t per = kRowThreads / 64;  // rows per workgroup
+    hipLaunchKernelGGL(fp8_quantize_rows_wave_kernel, dim3((unsigned)((rows + per - 1) / per)), dim3(kRowThreads), 0,
+                       (hipStream_t)stream, static_cast<const uint16_t*>(x), K, ldx, rows, q, scale);
+    return check_launch("fp8_quantize_rows");
+  }
   hipLaunchKernelGGL(fp8_quantize_rows_kernel, dim3((unsigned)rows), dim3(kRowThreads), 0,
                      (hipStream_t)stream, x, x_dtype, K, ldx, q, scale);
   return check_launch("fp8_quantize_rows");

@@ -65,12 +65,19 @@ def test_int4_symmetric_quantize_dequantize_bit_exact(shape, group):
     assert same_bytes(ops.int4_dequantize(q, s, None), O.int4_dequantize(**want))
 
 
+# bf16 rows of at most 4096 (multiples of 8) take the wavefront-per-row kernel, the others
+# the workgroup-per-row kernel; "wg" forces the latter everywhere (MIQ_FP8_QUANT_ROWS_WG)
 @pytest.mark.parametrize("shape,dtype,std", [((64, 256), torch.bfloat16, 0.02), ((2048, 2560), torch.bfloat16, 1.0),
                                              ((6144, 2560), torch.float32, 0.02), ((7, 200), torch.bfloat16, 3.0),
-                                             ((5, 8192), torch.bfloat16, 1.0), ((3, 8200), torch.bfloat16, 1.0)])
-def test_fp8_quantize_rows_bit_exact(shape, dtype, std):
+                                             ((5, 8192), torch.bfloat16, 1.0), ((3, 8200), torch.bfloat16, 1.0),
+                                             ((9, 4096), torch.bfloat16, 1.0), ((6, 4104), torch.bfloat16, 1.0),
+                                             ((1, 8), torch.bfloat16, 1.0)])
+@pytest.mark.parametrize("kernel", ["auto", "wg"])
+def test_fp8_quantize_rows_bit_exact(shape, dtype, std, kernel, miq_env):
     from kernels import quant_ops as ops
-    case(f"fp8 rows {shape} {dtype}")
+    case(f"fp8 rows {shape} {dtype} {kernel}")
+    if kernel == "wg":
+        miq_env("MIQ_FP8_QUANT_ROWS_WG", "1")
     x = weights(shape, 4, dtype, std)
     wq = O.fp8_quantize(x)
     q, s = ops.fp8_quantize_rows(x.to(DEV))
@@ -112,6 +119,13 @@ def test_fp8_quantize_rows_every_bf16_value():
     assert s.item() == 1.0
     want = O.fp8_quantize(row)
     assert same_bytes(q, want["qweight"])
+    # the same values in rows of 4096 (the wavefront-per-row kernel), each row with 448 so
+    # that every scale is 1
+    flat = torch.cat([vals, torch.zeros((-vals.numel()) % 4095, dtype=torch.bfloat16)]).reshape(-1, 4095)
+    rows = torch.cat([flat, torch.full((flat.shape[0], 1), 448.0, dtype=torch.bfloat16)], dim=1)
+    q2, s2 = ops.fp8_quantize_rows(rows.to(DEV))
+    assert (s2 == 1.0).all()
+    assert same_bytes(q2, O.fp8_quantize(rows)["qweight"])
     assert same_bytes(q, row.float().to(torch.float8_e4m3fn))
 
 
