@@ -20,6 +20,8 @@ Tuning read_tuning() {
   t.wo_stream = flag("MIQ_WO_STREAM");
   const char* rows = getenv("MIQ_WO_ROWS");
   t.wo_rows = rows ? atoi(rows) : 0;
+  const char* tmw = getenv("MIQ_WO_TILE_MIN_W");
+  t.wo_tile_min_w = tmw ? atoi(tmw) : 0;
   const char* pmin = getenv("MIQ_WO_PAIR_MIN_M");
   t.wo_pair_min_m = pmin ? atoi(pmin) : 0;
   const char* t2 = getenv("MIQ_WO_INT8_TILE2_MIN_M");

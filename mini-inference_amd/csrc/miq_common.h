@@ -187,6 +187,7 @@ int check_launch(const char* what);
 struct Tuning {
   bool wo_stream;             // MIQ_WO_STREAM: weight-only GEMMs take the streamed kernel
   int wo_rows;                // MIQ_WO_ROWS: rows per tile of the tile kernel (0: default)
+  int wo_tile_min_w;          // MIQ_WO_TILE_MIN_W: fewest wavefronts per tile workgroup (0: planned)
   int wo_pair_min_m;          // MIQ_WO_PAIR_MIN_M: the tile kernel's two-half int4 plan from
                               // this M up to 16 (0: default range, -1: never)
   int wo_int8_tile2_min_m;    // MIQ_WO_INT8_TILE2_MIN_M: int8 tile kernel with two row tiles per

@@ -54,6 +54,11 @@ using namespace wo;
 
 
 constexpr int kTileNS = 8;                 // k-steps in flight per wavefront (all of its slice)
+// k-steps a wavefront holds, by weight kind and row tiles: int8 with two row tiles holds 4
+// (the weight registers of 8 would leave one wavefront per SIMD). Int4 with 10 (K = 9728
+// then fits 8 wavefronts instead of 16) measured slower from M = 2 on (M = 1 / 2 / 4 / 6:
+// 6.6 / 7.2-7.3 / 8.6-8.7 / 10.3-10.7 against 6.5-6.8 / 6.8-6.9 / 8.1-8.3 / 9.5-9.6 us)
+constexpr int tile_ns(int kind, int nt) { return kind == KIND_INT8 && nt == 2 ? kTileNS / 2 : kTileNS; }
 constexpr int kTileLds = 160 * 1024;       // gfx950 LDS per workgroup
 constexpr int kCUs = 256;                  // MI355X compute units
 // int4: rows of the two-half plan by default. INT4 N = 2560, K = 9728 on MI355X, weights
@@ -102,7 +107,7 @@ wo_tile_kernel(TileParams p) {
   static_assert(KIND == KIND_INT4 || KS == 1, "int8 workgroups cover all of K");
   // k-steps in flight per wavefront: int8 with two row tiles holds 4 (the weight registers
   // of 8 would leave one wavefront per SIMD)
-  constexpr int NS = KIND == KIND_INT8 && NT == 2 ? kTileNS / 2 : kTileNS;
+  constexpr int NS = tile_ns(KIND, NT);
   constexpr int kThreads = W * 64, XP = tile_xp<KIND>();
   constexpr int kStepBytes = KIND == KIND_INT4 ? kStepK / 2 : kStepK;  // per weight row
   extern __shared__ __align__(16) uint16_t lds[];
@@ -180,13 +185,16 @@ wo_tile_kernel(TileParams p) {
   // the weights: the multiply of k-step d then waits only for the weight loads up to d
   // (loads complete in issue order), not for the last one
   constexpr int esz = SD == MIQ_F32 ? 4 : 2;
-  uint32_t sw[NT][8], zw[NT][8];
+  // words of the slice's group values: NS fp32 words, or up to NS / 2 + 1 words of 16-bit
+  // values (the first may sit in the high half), in 16-byte loads
+  constexpr int kSW = SD == MIQ_F32 ? (NS + 3) / 4 * 4 : 8;
+  uint32_t sw[NT][kSW], zw[NT][kSW];
   if (KIND == KIND_INT4) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int sbase = r < nrows[t] ? (soff[t] * esz) & ~3 : kOut - 32;
+      const int sbase = r < nrows[t] ? (soff[t] * esz) & ~3 : kOut - 64;
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < kSW / 4; ++h) {
         const auto v = __builtin_amdgcn_raw_buffer_load_b128(srs, sbase + 16 * h, 0, 0);
         const uint4 u = *reinterpret_cast<const uint4*>(&v);
         sw[t][4 * h] = u.x; sw[t][4 * h + 1] = u.y; sw[t][4 * h + 2] = u.z; sw[t][4 * h + 3] = u.w;
@@ -488,7 +496,7 @@ static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_s
   // (two row tiles per workgroup: 16-row pairs, 320 workgroups, measured 11.1 against
   // 9.6 us at M = 8)
   const int nt = int8_two ? 2 : ks;
-  const int ns = kind == KIND_INT8 && nt == 2 ? kTileNS / 2 : kTileNS;  // k-steps per wavefront at most
+  const int ns = tile_ns(kind, nt);  // k-steps per wavefront at most
   const int64_t xsteps = (units + ks - 1) / ks * us;  // k-steps staged per workgroup
   const int64_t xbytes = M * (xsteps * kStepK + 8) * 2;
   // rows per tile: 16 (MIQ_WO_ROWS overrides, tuning). With per-wavefront activation
@@ -500,7 +508,7 @@ static TilePlan plan_tile(int kind, int64_t M, int64_t N, int64_t K, int group_s
   const int64_t blocks = ks * ((N + rows * nt - 1) / (rows * nt));
   const int64_t wunits = (units + ks - 1) / ks;  // units per workgroup, at most
   for (int W : {4, 8, 16}) {
-    if ((wunits + W - 1) / W * us > ns) continue;
+    if ((wunits + W - 1) / W * us > ns || W < tuning().wo_tile_min_w) continue;
     const size_t lds = (size_t)std::max<int64_t>(xbytes, (int64_t)W * M * 16 * nt * 4) + (size_t)xsteps * 16 * 4;
     if (lds > (size_t)kTileLds) return pl;
     // every tile should be resident at once (a second wave of workgroups would stage the
