@@ -182,8 +182,8 @@ fp8_quantize_rows_kernel(const void* __restrict__ x, int x_dtype, int64_t K, int
   const int64_t row = blockIdx.x;
   const int64_t base = row * ldx;
   float amax = 0.f;
-  if (x_dtype == MIQ_BF16 && (K % 8) == 0 && (ldx % 8) == 0 &&
-      (reinterpret_cast<uintptr_t>(x) & 15) == 0) {
+  if (x_dtype == MIQ_BF16 && (K % 8) == 0 && (ldx % 8) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(q) & 7) == 0) {
     // the row's 8-element pieces: up to kHeld per thread stay in registers between the
     // max pass and the conversion pass (K <= 8192 at 256 threads), later ones are read again
     constexpr int kHeld = 4;
@@ -336,7 +336,8 @@ extern "C" int miq_fp8_quantize_rows(const void* x, int x_dtype, int64_t rows, i
   if (rows == 0) return MIQ_OK;
   MIQ_REQUIRE(rows <= 0x7fffffff, "fp8_quantize_rows: too many rows");
   if (x_dtype == MIQ_BF16 && K % 8 == 0 && K <= 64 * 8 * kWaveHeld && ldx % 8 == 0 &&
-      (reinterpret_cast<uintptr_t>(x) & 15) == 0 && !tuning().fp8_quant_rows_wg) {
+      (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(q) & 7) == 0 &&
+      !tuning().fp8_quant_rows_wg) {
     const int64_t per = kRowThreads / 64;  // rows per workgroup
     hipLaunchKernelGGL(fp8_quantize_rows_wave_kernel, dim3((unsigned)((rows + per - 1) / per)), dim3(kRowThreads), 0,
                        (hipStream_t)stream, static_cast<const uint16_t*>(x), K, ldx, rows, q, scale);
