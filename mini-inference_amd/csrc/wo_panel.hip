@@ -475,9 +475,12 @@ PanelPlan plan_panel(int64_t M, int64_t N, int64_t K, int group_steps) {
   const int64_t units = steps / unit;
   const int64_t per_max = kPanelSteps / unit;  // units one workgroup can take
   const int64_t s_min = (units + per_max - 1) / per_max;
-  // about one panel per CU (producers plus the extra reduce-only row block), times the
-  // activation groups
-  int64_t S = std::max<int64_t>(s_min, kCUs / (blocks + 1));
+  // about one panel per CU (producers plus the extra reduce-only row block), divided by
+  // the activation tiles a workgroup takes (Qwen3 down_proj on MI355X, weights from HBM:
+  // M = 64 with two tiles 18.9 us at 10 splits against 19.5 at 12 (0.1-0.2 us apart on another
+  // box), 26.1-26.6 at 14-16; M = 32
+  // with one tile 14.7-15.0 at 12 against 14.9-15.5 at 10)
+  int64_t S = std::max<int64_t>(s_min, kCUs / ((blocks + 1) * MT));
   if (tu.wo_panel_s > 0) S = std::max<int64_t>(s_min, tu.wo_panel_s);
   S = std::min<int64_t>(S, units);
   if (s_min > units) return pl;
