@@ -370,7 +370,7 @@ constexpr int kMoeD = 2;
 // LDS and forms the moe_align layout itself, for up to kRtPairs pairs and kRtExperts experts
 constexpr int kRtPairs = 1024, kRtExperts = 256;
 constexpr int kRtTiles = (kRtPairs + kRtExperts * (16 - 1) + 15) / 16;  // padded tiles at most
-constexpr size_t kMoeStaticLds = 4096;  // the streaming kernel's static LDS, rounded up
+constexpr size_t kMoeStaticLds = 4608;  // the streaming kernel's static LDS, rounded up
 constexpr int kMoeChunk = 16;  // k-steps of activations staged at once
 // FP8 experts (e4m3fn codes, one fp32 scale per weight row), next to wo_core's INT8 / INT4;
 // their activation rows are staged whole (K <= kF8Steps k-steps: one byte per code, so twice
@@ -389,8 +389,11 @@ constexpr int kMoeLdsGroups = 16;
 template <bool HZ>
 constexpr size_t kMoeScaleLdsPerWave = (size_t)2 * kMoeLdsGroups * kTile * (HZ ? 4 : 2);  // 2 tiles
 
+// eight-wavefront workgroups are held to 128 VGPRs (four wavefronts per SIMD, two
+// workgroups per CU; the routing code had taken the 8-bit down kernels to 132-140, one
+// workgroup per CU)
 template <int KIND, int MODE, bool HZ, int SD, bool G1, bool SL, int NW>
-__global__ void __launch_bounds__(NW * 64)
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(NW == 8 && KIND != KIND_INT4 ? 4 : 1)))
 moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
   constexpr int kThreads = NW * 64;
   extern __shared__ __align__(16) uint16_t lds[];
@@ -406,6 +409,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
   __shared__ uint16_t s_ids[kRtPairs];
   __shared__ int s_off[kRtExperts + 1];
   __shared__ uint16_t s_te[kRtTiles];       // expert of each padded tile
+  __shared__ uint16_t s_cnt[kRtExperts];    // pairs of each expert
   __shared__ int s_cc[kRtPairs / 64];       // hits of the current expert per 64-pair chunk
   __shared__ int s_pair[kTile];
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -418,7 +422,6 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
   const int64_t ngroups = B1 ? 1 : steps / p.group_steps;
   const uint16_t* xbase = MODE == MOE_GU ? p.hidden : p.hbuf;
   const int ldx = K;
-  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
   int npad;
   if (routed) {
     // the moe_align layout from topk_ids: pairs grouped by expert, each group padded to a
@@ -438,7 +441,9 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
       int carry = 0;
       for (int e0 = 0; e0 < p.E; e0 += 64) {
         const int e = e0 + lane;
-        const int c = e < p.E ? (s_off[e] + kTile - 1) / kTile * kTile : 0;
+        const int n = e < p.E ? s_off[e] : 0;
+        if (e < p.E) s_cnt[e] = (uint16_t)n;
+        const int c = (n + kTile - 1) / kTile * kTile;
         int incl = c;
         for (int o = 1; o < 64; o <<= 1) {
           const int up = __shfl_up(incl, o, 64);
@@ -577,6 +582,9 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
       // chunk adds the counts of the chunks before it.
       const int j0 = tile * kTile - s_off[e];
       const int nch = (p.num_pairs + 63) >> 6;
+      // Every write of s_pair / s_src comes after the barrier, which every wavefront reaches
+      // only after the previous item's epilogue (which reads s_pair): rows below the
+      // expert's pair count get their pair, the rows past it padding.
       uint64_t mk[kRtPairs / 64 / NW];
 #pragma unroll
       for (int q = 0; q < kRtPairs / 64 / NW; ++q) {
@@ -584,34 +592,43 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
         mk[q] = __ballot(c < nch && i < p.num_pairs && s_ids[i] == e);
         if (c < nch && lane == 0) s_cc[c] = __popcll(mk[q]);
       }
-      if (tid < kTile) {
+      __syncthreads();
+      if (tid < kTile && tid >= (int)s_cnt[e] - j0) {
         s_pair[tid] = p.num_pairs;
         s_src[tid] = -1;
       }
-      __syncthreads();
 #pragma unroll
       for (int q = 0; q < kRtPairs / 64 / NW; ++q) {
         const int c = wv + q * NW, i = c * 64 + lane;
         if (c >= nch) break;  // uniform
         int base = 0;
         for (int b = 0; b < c; ++b) base += s_cc[b];
-        const int m = base + __popcll(mk[q] & below) - j0;
+        // rank of this lane's pair among the chunk's pairs of e (the lanes below it with a
+        // hit: mbcnt on the ballot, no per-lane mask register)
+        const int m = base + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mk[q] >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)mk[q], 0u)) - j0;
         if (((mk[q] >> lane) & 1) && m >= 0 && m < kTile) {
           s_pair[m] = i;
           s_src[m] = MODE == MOE_GU ? i / p.topk : tile * kTile + m;
         }
       }
-    } else if (stage && tid < kTile) {
-      const int pair = p.sorted_ids[tile * kTile + tid];
-      s_pair[tid] = pair;
-      s_src[tid] = pair < p.num_pairs ? (MODE == MOE_GU ? pair / p.topk : tile * kTile + tid) : -1;
+    } else if (stage) {
+      // moe_align's layout from memory; the barrier orders the s_pair writes after the
+      // previous item's epilogue, as above
+      const int pair = tid < kTile ? p.sorted_ids[tile * kTile + tid] : 0;
+      __syncthreads();
+      if (tid < kTile) {
+        s_pair[tid] = pair;
+        s_src[tid] = pair < p.num_pairs ? (MODE == MOE_GU ? pair / p.topk : tile * kTile + tid) : -1;
+      }
     }
     __syncthreads();  // s_src ready (and the previous item is done with LDS)
-    // down: the pairs of this lane's output rows, read now (before the staging barrier,
-    // after which wavefront 0 may already fill s_pair for the next item)
+    // int4 down: the pairs of this lane's output rows, held in registers from here (the
+    // layer measured 0.6 us faster so); the 8-bit kinds read them at the end, their
+    // registers being at the 128 that four wavefronts per SIMD allow
     int lpair[4];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) lpair[v] = MODE == MOE_DN ? s_pair[g * 4 + v] : 0;
+    for (int v = 0; v < 4; ++v) lpair[v] = MODE == MOE_DN && KIND == KIND_INT4 ? s_pair[g * 4 + v] : 0;
     if constexpr (SL) {
       // (only this wavefront reads its slice, in program order after these writes)
 #pragma unroll
@@ -882,7 +899,7 @@ moe_stream_kernel(MoeParams p, int blocks_per_tile, int run) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int m = g * 4 + v;
-        const int pair = lpair[v];
+        const int pair = KIND == KIND_INT4 ? lpair[v] : s_pair[m];
         if (pair < p.num_pairs) {
           const float w = load_scalar(p.topk_w, p.w_dtype, pair);
           const int n0 = blk * (32 * NW) + wv * 32 + r;
