@@ -10,8 +10,12 @@
 // sizes whose chunk tables do not fit in LDS, one wavefront per expert walking the pairs.
 //
 // The grouped GEMMs reuse the weight-only core (wo_core.h): a workgroup takes one
-// 16-row tile of one expert, gathers its activation rows into LDS, and its four
-// wavefronts stream 16 weight rows each.
+// 16-row tile of one expert, gathers its activation rows into LDS, and its wavefronts
+// stream the weight rows (the streaming kernels: eight wavefronts of two 16-row tiles;
+// the tiled kernels: four of one). Routed launches (the *_routed entry points) give the
+// streaming kernels topk_ids instead of moe_align's arrays: every workgroup forms the same
+// layout in LDS (counts, padded offsets, each tile's expert and pairs), so no align
+// kernel runs.
 #include <stdlib.h>
 
 #include <algorithm>
