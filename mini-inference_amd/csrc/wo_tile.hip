@@ -22,7 +22,9 @@
 // word per output of the caller's zeroed workspace. Each swaps its fp32 sum in with one
 // agent-scope atomic exchange; the one that finds the other's sum adds the two (the same
 // bits in either order), writes y and clears the word, so there is one round trip and no
-// counter, and the workspace is all zeros again after the call.
+// counter, and the workspace is all zeros again after the call. INT8 at 4 and 5 rows takes
+// workgroups of two 16-row tiles over all of K, which share one staging of the activations
+// (no exchange).
 //
 // Per-element math is the one of the streamed kernel (wo_stream.hip): codes unpack to
 // bf16 128 + code, MFMA 16x16x32 bf16 with fp32 accumulation, and per quantization group
