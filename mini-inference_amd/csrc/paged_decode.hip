@@ -749,16 +749,19 @@ paged_decode_merge_kernel(const float* __restrict__ o_part, const float* __restr
                           uint16_t* __restrict__ out, int64_t os_b, int64_t os_h) {
   __shared__ float s_w[kD];
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const int64_t base = ((int64_t)b * H + h) * max_parts;
+  // the first kD slots' lse are requested with the context length (they do not depend on
+  // it; slots past the request's partitions are read and not used)
+  const float lse0 = d < max_parts ? lse_part[base + d] : -__builtin_inff();
   const int L = lens[b];
   const int span = partition_span(L, partition, max_parts);
   int np = (L + span - 1) / span;  // <= max_parts by the choice of span
   if (np < 1) np = 1;
-  const int64_t base = ((int64_t)b * H + h) * max_parts;
   float mx = -__builtin_inff(), den = 0.f, num = 0.f;
   for (int s0 = 0; s0 < np; s0 += kD) {  // kD partitions per round (one per thread)
     const int cnt = min(kD, np - s0);
     __syncthreads();
-    if (d < cnt) s_w[d] = lse_part[base + s0 + d];
+    if (d < cnt) s_w[d] = s0 == 0 ? lse0 : lse_part[base + s0 + d];
     __syncthreads();
     float m2 = mx;
     for (int i = 0; i < cnt; ++i) m2 = fmaxf(m2, s_w[i]);
