@@ -289,7 +289,9 @@ def bench_attention(dev, kind):
         gbs = a["bytes"] / t / 1e9
         res[f"partition_{partition}"] = {"us_per_step": round(t * 1e6, 2), "GB/s": round(gbs, 1),
                                          "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1)}
-    res["default_partition"] = 256
+    from kernels.paged_attention.decode import choose_partition
+    kc = a["caches"][0][0]
+    res["default_partition"] = choose_partition(a["max_len"], None, kc.dtype)
     del a
     return res
 

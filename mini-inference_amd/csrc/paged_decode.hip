@@ -391,7 +391,25 @@ template <int KVT, bool HAS_SCALE, int SD, int CS, int NC, int W, bool P16 = fal
 __global__ void __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(2)))
 paged_decode_split8_kernel(AttnParams p) {
   const int part = blockIdx.y, kvh = blockIdx.x, b = blockIdx.z;  // kv heads of one partition are dispatched together (they share DRAM pages)
+  // P16: the page ids of this wavefront's slice in the usual case (the partition covers
+  // partition tokens from part * partition), requested together with the context length
+  // rather than after it. Indices are clamped to the table's B rows of bt_stride entries;
+  // an id is used only where its page lies inside the context (else the ids are read again
+  // below, clamped to the last page).
+  constexpr int kWPS = P16 ? 4 : 1;  // the first 4 pages (the first two 32-token chunks)
+  int spec[kWPS];
+  const int spg0 = (part * p.partition + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) * (p.partition / W)) >> 4;
+  if constexpr (P16) {
+    const int64_t row0 = (int64_t)b * p.bt_stride, lim = (int64_t)gridDim.z * p.bt_stride - 1;
+#pragma unroll
+    for (int j = 0; j < kWPS; ++j) spec[j] = p.bt[min(row0 + spg0 + j, lim)];
+  }
   const int L = p.lens[b];
+  if constexpr (P16) {
+    // one use of the length and of every id together, so the compiler issues their loads
+    // back to back (it would otherwise sink the id loads below the length's branches)
+    asm volatile("" ::"s"(L), "s"(spec[0]), "s"(spec[1]), "s"(spec[2]), "s"(spec[3]));
+  }
   if (L <= 0) {
     if (part == 0) write_empty_split(p, b, kvh, W * 64);
     return;
@@ -478,8 +496,14 @@ paged_decode_split8_kernel(AttnParams p) {
   int wpage[kWP];
   if constexpr (P16) {
     const int wpg0 = t_begin >> 4, pg_last = (L - 1) >> 4;  // L >= 1 here
+    static_assert(kWP >= kWPS, "16-token pages: at least two 32-token chunks per wavefront");
+    if (wpg0 == spg0 && wpg0 + kWP - 1 <= pg_last) {  // every page of the slice is in the context
 #pragma unroll
-    for (int j = 0; j < kWP; ++j) wpage[j] = btrow[min(wpg0 + j, pg_last)];
+      for (int j = 0; j < kWP; ++j) wpage[j] = j < kWPS ? spec[j] : btrow[wpg0 + j];
+    } else {
+#pragma unroll
+      for (int j = 0; j < kWP; ++j) wpage[j] = btrow[min(wpg0 + j, pg_last)];
+    }
   }
 
   // ---- the pieces of one chunk of CS x 32 tokens starting at c0
