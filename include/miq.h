@@ -164,9 +164,10 @@ int miq_kv_quant_write(const void* x, int x_dtype, int64_t T, int64_t heads, int
  * [slots, KV, D] with kv_dtype MIQ_BF16 / MIQ_FP8_E4M3 / MIQ_INT8 (strides in elements);
  * k_scale/v_scale: NULL or [slots, KV] of scale_dtype with strides (s_stride_t,
  * s_stride_h) (0, 0 for one per-tensor value); block_table int32 [B, max_pages] row
- * stride bt_stride; seq_lens int32 [B]. D == 128.
+ * stride bt_stride, whose memory spans B * bt_stride entries (entries past a request's
+ * pages may be read, not used); seq_lens int32 [B]. D == 128.
  * The context of each request is cut into partitions of `partition` tokens (multiple of
- * 64). Workspace: o_part fp32 [B, H, max_parts, D] and lse_part fp32 [B, H, max_parts],
+ * 128). Workspace: o_part fp32 [B, H, max_parts, D] and lse_part fp32 [B, H, max_parts],
  * max_parts >= ceil(max(seq_lens) / partition). */
 int miq_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h,
                      const void* k_cache, const void* v_cache, int kv_dtype,
