@@ -42,6 +42,22 @@ enum miq_dtype {
 const char* miq_last_error(void);
 int miq_abi_version(void);
 
+/* Device-side failures that a kernel cannot return as a status: bits of a per-GPU error
+ * word that kernels set and miq_device_errors() reads. No counterpart in the reference
+ * (its kernels have no bounded waits). */
+enum miq_device_error {
+  MIQ_DEVERR_PANEL_WAIT = 1, /* the INT4 panel GEMM's split-K reducer gave up waiting for a
+                                partial; the affected outputs were written as NaN */
+};
+
+/* Waits for `stream`, stores the current device's error word in *bits and clears it.
+ * A diagnostic for tests and health checks: it synchronises, unlike every other entry
+ * point. No counterpart in the reference. */
+int miq_device_errors(unsigned* bits, void* stream);
+
+/* Text for error word `bits` (host only, needs no GPU). */
+const char* miq_device_error_string(unsigned bits);
+
 /* Re-reads the MIQ_* kernel-selection variables (MIQ_WO_STREAM, MIQ_WO_PANEL, ...), which
  * the library otherwise reads once when it is loaded. No counterpart in the reference: a
  * hook for tests and tuning runs that switch kernels inside one process. Not to be

@@ -34,8 +34,6 @@ Tuning read_tuning() {
   t.wo_panel_s = ps ? atoi(ps) : 0;
   const char* pm = getenv("MIQ_WO_PANEL_MT");
   t.wo_panel_mt = pm ? atoi(pm) : 0;
-  const char* pa = getenv("MIQ_WO_PANEL_ABL");
-  t.wo_panel_abl = pa ? atoi(pa) : 0;
   const char* pmm = getenv("MIQ_WO_PREFILL_MIN_M");
   t.wo_prefill_min_m = pmm && atoi(pmm) > 0 ? atoi(pmm) : 65;
   const char* pps = getenv("MIQ_WO_PREFILL_S");
@@ -80,9 +78,53 @@ int check_launch(const char* what) {
 
 }  // namespace miq
 
+namespace miq {
+namespace {
+__device__ unsigned g_device_error;  // one word per GPU, zero until a kernel reports a failure
+constexpr int kMaxDevices = 64;
+std::mutex g_error_word_lock;
+unsigned* g_error_word[kMaxDevices];
+}  // namespace
+
+unsigned* device_error_word() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> hold(g_error_word_lock);
+  if (!g_error_word[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_device_error)) != hipSuccess) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    g_error_word[dev] = static_cast<unsigned*>(ptr);
+  }
+  return g_error_word[dev];
+}
+}  // namespace miq
+
 extern "C" const char* miq_last_error(void) { return miq::g_error; }
 
-extern "C" int miq_abi_version(void) { return 3; }
+extern "C" const char* miq_device_error_string(unsigned bits) {
+  if (bits == 0) return "no device error";
+  if (bits == MIQ_DEVERR_PANEL_WAIT) return "INT4 panel GEMM: a split-K reducer gave up waiting for a partial (NaN written)";
+  return "unknown device error bits";
+}
+
+extern "C" int miq_device_errors(unsigned* bits, void* stream) {
+  MIQ_REQUIRE(bits != nullptr, "miq_device_errors: bits is NULL");
+  unsigned* word = miq::device_error_word();
+  MIQ_REQUIRE(word != nullptr, "miq_device_errors: no device error word on this device");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned zero = 0;
+  if (hipStreamSynchronize(st) != hipSuccess || hipMemcpy(bits, word, sizeof(unsigned), hipMemcpyDeviceToHost) != hipSuccess ||
+      hipMemcpy(word, &zero, sizeof(unsigned), hipMemcpyHostToDevice) != hipSuccess) {
+    miq::set_error("miq_device_errors: %s", hipGetErrorString(hipGetLastError()));
+    return MIQ_ERR_LAUNCH;
+  }
+  return MIQ_OK;
+}
+
+extern "C" int miq_abi_version(void) { return 4; }
 
 extern "C" int miq_tuning_reload(void) {
   std::lock_guard<std::mutex> hold(miq::g_tuning_lock);

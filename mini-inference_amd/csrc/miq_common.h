@@ -199,7 +199,6 @@ struct Tuning {
   int wo_panel;               // MIQ_WO_PANEL: 0 off, 1 forced where it applies, -1 default
   int wo_panel_s;             // MIQ_WO_PANEL_S: K splits of the panel kernel (0: planned)
   int wo_panel_mt;            // MIQ_WO_PANEL_MT: activation tiles per panel workgroup (1, 2, 4)
-  int wo_panel_abl;           // MIQ_WO_PANEL_ABL: ablation runs (timing only; wrong results)
   int wo_prefill_min_m;       // MIQ_WO_PREFILL_MIN_M: smallest M for the prefill kernel (65)
   int wo_prefill_s;           // MIQ_WO_PREFILL_S: K splits of the prefill kernel (0: planned)
   bool fp8_old;               // MIQ_FP8_OLD: the previous FP8 GEMM kernel family
@@ -213,6 +212,11 @@ struct Tuning {
 };
 const Tuning& tuning();
 
+// The current device's error word (bits MIQ_DEVERR_*): kernels that detect a condition
+// they cannot report through a return code set a bit here; miq_device_errors() reads and
+// clears it. The address comes from hipGetSymbolAddress once per device.
+unsigned* device_error_word();
+
 // Raises a kernel's dynamic LDS limit to what gfx950's 160 KiB leaves beside its static
 // LDS; call once per kernel (a rejected request would otherwise linger as the error the
 // next launch check reports, so any error of these calls is consumed here).
@@ -223,6 +227,11 @@ inline void allow_max_dynamic_lds(const void* kernel) {
   (void)hipGetLastError();
 }
 }  // namespace miq
+
+// Sets `bits` in the device error word (a vector atomic; never a scalar-cache store).
+__device__ inline void raise_device_error(unsigned* word, unsigned bits) {
+  if (word) __hip_atomic_fetch_or(word, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 #define MIQ_REQUIRE(cond, ...)                 \
   do {                                         \

@@ -883,6 +883,9 @@ extern "C" int miq_paged_decode(const void* q, int64_t q_stride_b, int64_t q_str
   MIQ_REQUIRE(partition >= 128 && partition % 128 == 0, "paged_decode: partition must be a multiple of 128");
   MIQ_REQUIRE(page >= 1 && B >= 1 && max_parts >= 1 && B < 65536 && KV < 65536 && max_parts < (1 << 30),
               "paged_decode: bad sizes");
+  MIQ_REQUIRE(bt_stride >= 1 && block_table != nullptr && seq_lens != nullptr,
+              "paged_decode: block_table needs a row stride >= 1 (got %lld); its memory spans B * bt_stride entries",
+              (long long)bt_stride);
   MIQ_REQUIRE((k_scale == nullptr) == (v_scale == nullptr), "paged_decode: give both scales or neither");
   MIQ_REQUIRE(kv_dtype != MIQ_BF16 || k_scale == nullptr, "paged_decode: bf16 cache takes no scales");
   MIQ_REQUIRE(scale_dtype == MIQ_F32 || scale_dtype == MIQ_BF16 || scale_dtype == MIQ_F16,

@@ -37,6 +37,12 @@
 #ifndef MIQ_TRACE
 #define MIQ_TRACE(point)  // per-workgroup timestamps in probe builds
 #endif
+// Ablation bits for timing probes, compiled in only with -DMIQ_PANEL_ABL=<bits> (the
+// results are then wrong): 1 no reduction, 2 no partial stores, 4 no activation loads,
+// 16 no multiply. The shipped library is built with 0.
+#ifndef MIQ_PANEL_ABL
+#define MIQ_PANEL_ABL 0
+#endif
 
 namespace miq {
 namespace {
@@ -70,9 +76,9 @@ struct PanelParams {
   int wbytes, sbytes, xbytes;
   float* partial;       // [S][N][Mp] marked fp32 words (Mp = M rounded up to 4)
   int Mp;
-  int abl;              // ablation bits (timing runs only, wrong results): 1 no reduction, 2 no partial
-                        // stores, 4 no activation loads, 8 no LDS pass, 16 no multiply
+  unsigned* error;      // device error word: set when a reducer gives up waiting
 };
+constexpr int kAbl = MIQ_PANEL_ABL;
 
 // A partial as stored: the bits of v + 0 (so -0 becomes +0) with the sign bit flipped,
 // which is never the all-zero word; the workspace holds zeros where no partial is pending.
@@ -97,7 +103,7 @@ __device__ __forceinline__ void produce(const PanelParams& p, int rb, int s, int
   const int ipr = (xcols + 63) / 64;     // loads of up to 64 pieces per row
   const __amdgpu_buffer_rsrc_t xrs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.x), 0, p.xbytes, 0x00020000);
-  for (int q = wv; q < ((p.abl & 4) ? 0 : M * ipr); q += W) {
+  for (int q = wv; q < ((kAbl & 4) ? 0 : M * ipr); q += W) {
     const int m = q / ipr, c0 = (q - m * ipr) * 64;
     if (c0 + lane < xcols)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -199,7 +205,7 @@ __device__ __forceinline__ void produce(const PanelParams& p, int rb, int s, int
   for (int mt = 0; mt < MT; ++mt) xsg[mt] = z4;
   int c_grp = 0, c_left = p.group_steps;
   uint4 wnext[NR];
-  if (p.abl & 16) {  // ablation: the weights are consumed without a multiply
+  if (kAbl & 16) {  // ablation: the weights are consumed without a multiply
     uint32_t z = 0;
 #pragma unroll
     for (int d = 0; d < NS; ++d)
@@ -209,7 +215,7 @@ __device__ __forceinline__ void produce(const PanelParams& p, int rb, int s, int
   }
 #pragma unroll
   for (int d = 0; d < NS; ++d) {
-    if (d < nst && !(p.abl & 16)) {
+    if (d < nst && !(kAbl & 16)) {
       bf16x8 av[MT][4];
       f32x4 xb[MT];
 #pragma unroll
@@ -314,7 +320,7 @@ __device__ __forceinline__ void produce(const PanelParams& p, int rb, int s, int
 #pragma unroll
         for (int v = 0; v < 4; ++v)
           if (mv + v < M) p.y[(int64_t)(m0 + mv + v) * p.ldy + n] = f32_to_bf16(acc[t][mt][v]);
-      } else if (!(p.abl & 2)) {
+      } else if (!(kAbl & 2)) {
         const i32x4 w4 = {(int)mark_partial(acc[t][mt][0]), (int)mark_partial(acc[t][mt][1]),
                           (int)mark_partial(acc[t][mt][2]), (int)mark_partial(acc[t][mt][3])};
         __builtin_amdgcn_raw_buffer_store_b128(w4, prs, (int)((((int64_t)s * p.N + n) * p.Mp + m0 + mv) * 4), 0,
@@ -345,6 +351,7 @@ __device__ __forceinline__ void reduce(const PanelParams& p, int rb, int s, int 
       __builtin_amdgcn_make_buffer_rsrc(p.partial, 0, (int)((int64_t)S * p.N * p.Mp * 4), 0x00020000);
   const int sstride = p.N * p.Mp * 4;
   int spins = 0;
+  bool gave_up = false;
   for (int v = v0 + tid; v < v1; v += kThreads) {
     const int c = v / nm4, m = (v - c * nm4) * 4, n = rb * ROWS + c;
     if (n >= p.N) continue;
@@ -375,6 +382,15 @@ __device__ __forceinline__ void reduce(const PanelParams& p, int rb, int s, int 
         for (int u = 0; u < kChunk; ++u)
           if (pending(u)) load(u);
       }
+      if (spins >= kSpinLimit) {
+        // a producer never arrived (it cannot happen while every lower workgroup id runs
+        // to completion): report it through the device error word and write NaN, never a
+        // sum with a missing partial
+        bool any = false;
+#pragma unroll
+        for (int u = 0; u < kChunk; ++u) any |= pending(u);
+        gave_up |= any;
+      }
       if (sp0 == 0) MIQ_TRACE(6);
       const i32x4 zero4 = {0, 0, 0, 0};
 #pragma unroll
@@ -386,6 +402,10 @@ __device__ __forceinline__ void reduce(const PanelParams& p, int rb, int s, int 
         o.w += unmark_partial(t[u].w);
         __builtin_amdgcn_raw_buffer_store_b128(zero4, prs, off + (sp0 + u) * sstride, 0, 16 /* sc1 */);
       }
+    }
+    if (gave_up) {
+      o = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""));
+      raise_device_error(p.error, MIQ_DEVERR_PANEL_WAIT);
     }
     uint16_t* yp = p.y + (int64_t)(m0 + m) * p.ldy + n;
     const float ov[4] = {o.x, o.y, o.z, o.w};
@@ -409,7 +429,7 @@ wo_panel_kernel(PanelParams p) {
   MIQ_TRACE(0);
   if (rb < p.blocks) produce<HZ, SD, MT, NR, G1>(p, rb, s, mg, lds);
   MIQ_TRACE(5);
-  if (p.S > 1 && rb >= 1 && !p.abl) reduce<MT, NR>(p, rb - 1, s, mg);
+  if (p.S > 1 && rb >= 1 && !kAbl) reduce<MT, NR>(p, rb - 1, s, mg);
   MIQ_TRACE(7);
 }
 
@@ -549,7 +569,7 @@ int wo_panel_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ld
   const int esz = sd == MIQ_F32 ? 4 : 2;
   p.sbytes = (int)(((int64_t)N * ngroups * esz + 3) & ~3LL);
   p.xbytes = (int)((int64_t)M * ldx * 2);
-  p.abl = tuning().wo_panel_abl;
+  p.error = device_error_word();
   p.partial = workspace ? reinterpret_cast<float*>(static_cast<char*>(workspace) + skip) : nullptr;
   p.groups = pl.groups;
   p.panels = pl.S > 1 ? (pl.blocks + 1) * pl.S : pl.blocks;

@@ -2,7 +2,8 @@
 
 Interface of the reference's engine/core/kv_cache.py (the storage half, :6-35 and
 :305-425): the format names "fp8" / "int8", `resolve_kv_dtype`, `kv_bytes_per_token`,
-`tokens_for_budget`, and `KVCache` with `write`, `gather`, `decode_tables`, `memory_mb`.
+`tokens_for_budget`, the two allocators (`PagedAllocator`, `ContiguousAllocator`), and
+`KVCache` with the allocator wrappers, `write`, `gather`, `decode_tables`, `memory_mb`.
 
 Layout (the reference's, so the paged-attention kernels read it as is):
   k, v                [layers, slots, kv_heads, head_dim] in the storage dtype
@@ -10,9 +11,14 @@ Layout (the reference's, so the paged-attention kernels read it as is):
   slot                page_id * block_size + position in the page
 
 `write` is one fused kernel per tensor (amax, bf16 scale, encode, scatter by slot).
-The reference's page allocators (free lists, prefix caching) belong to its serving
-engine and are not rebuilt here: callers hand in slots and page lists.
+The allocators keep the reference's bookkeeping contract (`tables[request id]` = the
+block table of a paged cache, `ranges[request id]` = (base, size) of a contiguous one,
+`slots`, `admit` / `reserve` / `ensure` / `free`), which is what `decode_tables` and the
+runner read. Prefix caching and the admission watermark belong to the reference's
+scheduler and are not rebuilt: `register` is a no-op and `admit` reports 0 cached tokens.
 """
+import bisect
+from collections import deque
 from typing import NamedTuple
 
 import torch
@@ -79,19 +85,210 @@ def kv_quant_write(cache, scale, slots, x):
                scale.stride(0), scale.stride(1), L.stream(x.device))
 
 
-class KVCache:
-    """Paged KV storage for all layers (reference kv_cache.py:305-425, storage part).
+def _cdiv(a, b):
+    return -(-a // b)
 
-    Only mode="paged" exists here; capacity is rounded down to whole blocks. The
-    `watermark` and `prefix_caching` arguments belong to the reference's allocator and
-    are accepted for signature compatibility."""
+
+class PagedAllocator:
+    """Fixed-size blocks handed out from a free list (reference kv_cache.py:124-300, without
+    prefix caching). `tables[request id]` is the request's block table: block i holds
+    positions i * block_size .. (i + 1) * block_size - 1."""
+
+    name = "paged"
+
+    def __init__(self, capacity, block_size):
+        self.block_size = block_size
+        self.num_blocks = capacity // block_size
+        self.capacity = self.num_blocks * block_size
+        self._free = deque(range(self.num_blocks))
+        self.tables = {}
+        self.length = {}
+
+    def blocks_for(self, num_tokens):
+        return _cdiv(num_tokens, self.block_size)
+
+    def can_admit(self, req, max_len):
+        return self.blocks_for(min(_total_len(req), max_len)) <= len(self._free)
+
+    def admit(self, req, max_len, size=None):
+        """Registers the request with an empty table; 0 tokens are cached already (None
+        when its current length does not fit)."""
+        if not self.can_admit(req, max_len):
+            return None
+        self.tables[req.id], self.length[req.id] = [], 0
+        return 0
+
+    def reserve(self, req, num_tokens):
+        table = self.tables.setdefault(req.id, [])
+        need = self.blocks_for(num_tokens) - len(table)
+        if need > len(self._free):
+            return False
+        table.extend(self._free.popleft() for _ in range(max(need, 0)))
+        return True
+
+    def ensure(self, req, num_tokens):
+        if not self.reserve(req, num_tokens):
+            return False
+        self.length[req.id] = num_tokens
+        return True
+
+    def free(self, req):
+        self._free.extend(self.tables.pop(req.id, ()))
+        self.length.pop(req.id, None)
+
+    def slots(self, req, start, end):
+        pos = torch.arange(start, end)
+        blocks = torch.tensor(self.tables[req.id], dtype=torch.long)
+        return blocks[pos // self.block_size] * self.block_size + pos % self.block_size
+
+    def stored_tokens(self):
+        return sum(self.length.values())
+
+
+class ContiguousAllocator:
+    """One first-fit range of slots per request, sized at admission (reference
+    kv_cache.py:50-121). `ranges[request id]` = (first slot, size)."""
+
+    name = "contiguous"
+
+    def __init__(self, capacity):
+        self.capacity = capacity
+        self._holes = [(0, capacity)]  # sorted (start, size) of free ranges
+        self.ranges = {}
+        self.length = {}
+
+    def _hole_for(self, size):
+        return next((i for i, (_, n) in enumerate(self._holes) if n >= size), None)
+
+    def can_admit(self, req, max_len):
+        return self._hole_for(min(_max_total_len(req), max_len)) is not None
+
+    def admit(self, req, max_len, size=None):
+        size = size or min(_max_total_len(req), max_len)
+        i = self._hole_for(size)
+        if i is None:
+            return None
+        start, n = self._holes.pop(i)
+        if n > size:
+            self._holes.insert(i, (start + size, n - size))
+        self.ranges[req.id], self.length[req.id] = (start, size), 0
+        return 0
+
+    def reserve(self, req, num_tokens):
+        return num_tokens <= self.ranges[req.id][1]
+
+    def ensure(self, req, num_tokens):
+        if not self.reserve(req, num_tokens):
+            return False
+        self.length[req.id] = num_tokens
+        return True
+
+    def free(self, req):
+        if req.id not in self.ranges:
+            return
+        start, size = self.ranges.pop(req.id)
+        self.length.pop(req.id, None)
+        # merge with the free range that ends at `start` and the one that begins at its end
+        holes, lo, hi = self._holes, start, start + size
+        i = bisect.bisect(holes, (start, size))
+        if i < len(holes) and holes[i][0] == hi:
+            hi += holes.pop(i)[1]
+        if i > 0 and sum(holes[i - 1]) == lo:
+            i -= 1
+            lo = holes.pop(i)[0]
+        holes.insert(i, (lo, hi - lo))
+
+    def slots(self, req, start, end):
+        base = self.ranges[req.id][0]
+        return torch.arange(base + start, base + end)
+
+    def stored_tokens(self):
+        return sum(self.length.values())
+
+
+def _total_len(req):
+    return getattr(req, "total_len", None) or len(req.all_ids)
+
+
+def _max_total_len(req):
+    return getattr(req, "max_total_len", None) or _total_len(req)
+
+
+def make_allocator(mode, capacity_tokens, block_size=16):
+    if mode == "paged":
+        return PagedAllocator(capacity_tokens, block_size)
+    if mode == "contiguous":
+        return ContiguousAllocator(capacity_tokens)
+    raise ValueError(f"Unknown KV_CACHE '{mode}' (use 'contiguous' or 'paged')")
+
+
+def pack_block_tables(tables, lens, device):
+    """Per-request page lists and context lengths -> (block_table int32 [B, width], zero
+    padded, seq_lens int32 [B]) on `device`, the paged-attention kernel's operands."""
+    width = max(1, max(len(t) for t in tables))
+    table = torch.zeros(len(tables), width, dtype=torch.int32)
+    for row, ids in enumerate(tables):
+        if ids:
+            table[row, : len(ids)] = torch.as_tensor(ids, dtype=torch.int32)
+    return table.to(device), torch.tensor(list(lens), dtype=torch.int32).to(device)
+
+
+class CacheBookkeeping:
+    """The allocator half of KVCache: thin wrappers (reference kv_cache.py:337-356) and the
+    kernel tables of a decode batch. Needs `self.allocator` and `self.mode`."""
+
+    def can_admit(self, req, max_len):
+        return self.allocator.can_admit(req, max_len)
+
+    def admit(self, req, max_len, size=None):
+        return self.allocator.admit(req, max_len, size)
+
+    def reserve(self, req, num_tokens):
+        return self.allocator.reserve(req, num_tokens)
+
+    def ensure(self, req, num_tokens):
+        return self.allocator.ensure(req, num_tokens)
+
+    def free(self, req):
+        self.allocator.free(req)
+
+    def register(self, req):
+        """After a step (prefix caching in the reference; nothing to publish here)."""
+
+    def slots(self, req, start, end):
+        return self.allocator.slots(req, start, end)
+
+    def decode_tables(self, entries, device):
+        """Page tables for the paged decode-attention kernel (reference kv_cache.py:403-420).
+        entries: (request, context_length) pairs. Returns (block_table int32 [B, pages],
+        seq_lens int32 [B], page_size, max_len). A paged cache hands over each request's
+        block table cut to its context (page = block size); a contiguous one describes its
+        range token by token (page = 1)."""
+        lens = [n for _, n in entries]
+        if self.mode == "paged":
+            a = self.allocator
+            tables = [a.tables[r.id][: a.blocks_for(n)] for r, n in entries]
+            page = a.block_size
+        else:
+            span = max(lens)
+            tables = [list(range(self.allocator.ranges[r.id][0], self.allocator.ranges[r.id][0] + span))
+                      for r, _ in entries]
+            page = 1
+        table, seq_lens = pack_block_tables(tables, lens, device)
+        return table, seq_lens, page, max(lens)
+
+class KVCache(CacheBookkeeping):
+    """KV storage for all layers with its allocator (reference kv_cache.py:305-425).
+
+    mode "paged": blocks of `block_size` slots (capacity rounded down to whole blocks);
+    "contiguous": one range per request. `watermark` and `prefix_caching` belong to the
+    reference's scheduler policy and are accepted for signature compatibility."""
 
     def __init__(self, mode, num_layers, num_kv_heads, head_dim, capacity_tokens, dtype, device,
                  block_size=16, watermark=0.01, kv_dtype=None, prefix_caching=False):
-        if mode != "paged":
-            raise ValueError("only the paged storage layout is provided (mode='paged')")
+        self.allocator = make_allocator(mode, capacity_tokens, block_size)
         self.mode, self.block_size, self.model_dtype = mode, block_size, dtype
-        self.capacity = capacity_tokens - capacity_tokens % block_size
+        self.capacity = self.allocator.capacity
         self.kv_dtype = resolve_kv_dtype(kv_dtype)
         dims = (num_layers, self.capacity, num_kv_heads, head_dim)
         fmt = KV_FORMATS.get(self.kv_dtype)
@@ -129,17 +326,6 @@ class KVCache:
         for codes, scale in ((self.k, self.k_scale), (self.v, self.v_scale)):
             out.append(self._codes(codes, layer, idx).to(self.model_dtype) * scale[layer][idx].unsqueeze(-1))
         return tuple(out)
-
-    @staticmethod
-    def decode_tables(pages, lens, block_size, device):
-        """Kernel tables for a decode batch (reference kv_cache.py:403-420, paged case):
-        page lists and context lengths -> (block_table int32 [B, width] zero-padded,
-        seq_lens int32 [B], page_size, max_len)."""
-        used = [list(p)[: (n + block_size - 1) // block_size] for p, n in zip(pages, lens)]
-        table = torch.zeros(len(used), max(map(len, used)), dtype=torch.int32)
-        for row, ids in enumerate(used):
-            table[row, : len(ids)] = torch.tensor(ids, dtype=torch.int32)
-        return table.to(device), torch.tensor(list(lens), dtype=torch.int32).to(device), block_size, max(lens)
 
     def memory_mb(self):
         """MiB of device memory the cache tensors hold."""

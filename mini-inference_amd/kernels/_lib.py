@@ -5,6 +5,7 @@ passes raw device pointers, element strides and torch's current HIP stream; the 
 allocates nothing. A missing library, a CPU tensor or a failed call raises RuntimeError:
 there is no host fallback on this path.
 """
+import collections
 import ctypes
 import os
 import threading
@@ -15,7 +16,7 @@ _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 LIB_PATH = os.environ.get("MIQ_LIB", os.path.join(_PKG_DIR, "libmiq.so"))
 
 MIQ_F32, MIQ_BF16, MIQ_F16, MIQ_FP8_E4M3, MIQ_INT8, MIQ_UINT8, MIQ_INT32, MIQ_INT64 = range(8)
-ABI_VERSION = 3  # miq_abi_version() of the library these signatures describe
+ABI_VERSION = 4  # miq_abi_version() of the library these signatures describe
 
 _DTYPE_CODES = {
     torch.float32: MIQ_F32,
@@ -35,6 +36,8 @@ SIGNATURES = {
     "miq_last_error": (ctypes.c_char_p, []),
     "miq_abi_version": (_I32, []),
     "miq_tuning_reload": (_I32, []),
+    "miq_device_errors": (_I32, [_P, _P]),
+    "miq_device_error_string": (ctypes.c_char_p, [ctypes.c_uint]),
     "miq_int8_quantize": (_I32, [_P, _I32, _I64, _I64, _I64, _P, _P, _I32, _P]),
     "miq_int8_dequantize": (_I32, [_P, _P, _I32, _I64, _I64, _P, _P]),
     "miq_int4_quantize": (_I32, [_P, _I32, _I64, _I64, _I64, _I64, _P, _P, _P, _I32, _P]),
@@ -122,21 +125,43 @@ def call(name, *args):
         raise RuntimeError(f"{name} failed ({rc}): {msg}")
 
 
+def device_error_text(bits):
+    """The library's description of device error word `bits` (host only)."""
+    return load().miq_device_error_string(bits).decode(errors="replace")
+
+
+def check_device_errors(device=None):
+    """Wait for the current stream of `device`, then raise RuntimeError if any kernel set a
+    bit of the device error word since the last check (the word is cleared). A diagnostic
+    for tests and health checks: it synchronises."""
+    device = torch.device("cuda") if device is None else device
+    bits = ctypes.c_uint(0)
+    call("miq_device_errors", ctypes.byref(bits), stream(device))
+    if bits.value:
+        raise RuntimeError(f"libmiq device error 0x{bits.value:x}: {device_error_text(bits.value)}")
+
+
 # ---------------------------------------------------------------- workspaces
 # Zero-initialised buffers for the split-K counters / partials of the weight-only GEMMs,
 # one per (device, stream): kernels leave the counters at zero, so a buffer is reused as
 # is by the launches of its stream, which run one after another. Two streams never share
 # one (concurrent launches would race on the counters). A buffer only grows (a new zeroed
 # buffer) when a larger shape comes along; the old one is released by the caching
-# allocator in the stream order of its last use.
-_wo_ws = {}
+# allocator in the stream order of its last use. At most _WO_WS_MAX buffers are kept (the
+# least recently used one is dropped, and the caching allocator reuses its memory only on
+# the stream it was allocated on, after the work queued there). A stream handle that HIP
+# recycles finds a buffer that is still all zero: every call leaves it so.
+_WO_WS_MAX = 8
+_wo_ws = collections.OrderedDict()
 
 
 def wo_workspace(device, nbytes):
     st = torch.cuda.current_stream(device)
     key = (device.type, device.index, st.cuda_stream)
-    buf = _wo_ws.get(key)
+    buf = _wo_ws.pop(key, None)
     if buf is None or buf.numel() < nbytes:
         buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _wo_ws[key] = buf
+    _wo_ws[key] = buf
+    while len(_wo_ws) > _WO_WS_MAX:
+        _wo_ws.popitem(last=False)
     return buf

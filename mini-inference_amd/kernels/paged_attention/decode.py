@@ -67,6 +67,10 @@ def paged_decode_attention(q, k_cache, v_cache, block_table, seq_lens, page_size
         raise ValueError("k_scale and v_scale must share strides")
     if block_table.dtype != torch.int32:
         block_table = block_table.to(torch.int32)
+    if not block_table.is_contiguous():
+        # the kernel reads page ids ahead of need, anywhere in B * stride(0) entries: an
+        # expanded (stride 0) or column-sliced table is copied to a dense one first
+        block_table = block_table.contiguous()
     if seq_lens.dtype != torch.int32:
         seq_lens = seq_lens.to(torch.int32)
     if max_len is None:

@@ -20,6 +20,7 @@ import copy
 import torch
 from torch import nn
 
+from engine.core.kv_cache import CacheBookkeeping, make_allocator
 from oracle import quant as Q
 from oracle.attention import paged_decode_reference
 from oracle.moe import int4_experts_reference, quant_experts_loop
@@ -133,11 +134,15 @@ def oracle_model(model, dtype=torch.float32):
     return cpu.eval()
 
 
-class OracleKVCache:
-    """engine/core/kv_cache.py:305-420 storage on the CPU with the restated quantizer."""
+class OracleKVCache(CacheBookkeeping):
+    """engine/core/kv_cache.py:305-420 storage on the CPU with the restated quantizer. Slot
+    bookkeeping (which slots a request owns, its block table) is the product's host-side
+    allocator: it decides where values go, not what they are."""
 
     def __init__(self, num_layers, num_kv_heads, head_dim, capacity_tokens, dtype=torch.float32, kv_dtype=None,
-                 scale_dtype=torch.bfloat16):
+                 scale_dtype=torch.bfloat16, mode="paged", block_size=16):
+        self.mode = mode
+        self.allocator = make_allocator(mode, capacity_tokens, block_size)
         self.kv_dtype = kv_dtype
         self.model_dtype = dtype
         self.scale_dtype = scale_dtype
@@ -177,13 +182,6 @@ class OracleKVCache:
             q = c.view(torch.uint8)[idx].view(Q.FP8) if c.dtype == Q.FP8 else c[idx]
             out.append(Q.kv_dequantize(q, scale[layer][idx]).to(self.model_dtype))
         return tuple(out)
-
-    @staticmethod
-    def decode_tables(pages, lens, block_size, device):
-        tables = [list(p[: -(-n // block_size)]) for p, n in zip(pages, lens)]
-        width = max(len(t) for t in tables)
-        table = torch.tensor([t + [0] * (width - len(t)) for t in tables], dtype=torch.int32)
-        return table, torch.tensor(lens, dtype=torch.int32), block_size, max(lens)
 
 
 def oracle_decode_attention(q, k_cache, v_cache, block_table, seq_lens, page_size, scale, max_len=None,

@@ -39,3 +39,15 @@ def miq_env(monkeypatch):
     yield setenv
     monkeypatch.undo()
     reload()
+
+
+@pytest.fixture(autouse=True)
+def _no_device_errors(request):
+    """After every GPU test: no kernel may have set a bit of libmiq's device error word
+    (a bounded wait that gave up and wrote NaN instead of a result)."""
+    yield
+    if "gpu" in request.keywords:
+        import torch
+        if torch.cuda.is_available():
+            from kernels import _lib
+            _lib.check_device_errors()

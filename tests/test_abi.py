@@ -45,7 +45,7 @@ def test_ctypes_table_matches_header():
 def test_abi_version_and_error_string():
     from kernels import _lib
     lib = _lib.load()
-    assert lib.miq_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.miq_abi_version() == _lib.ABI_VERSION == 4
     assert lib.miq_tuning_reload() == 0
     # a shape error is reported without touching the GPU
     rc = lib.miq_w8a16_gemm(None, 0, None, None, 0, None, 0, 0, 16, 128, None, 0, None)
@@ -72,3 +72,15 @@ def test_cpu_tensors_are_refused():
     with pytest.raises(RuntimeError, match="ROCm device tensors only"):
         paged_decode_attention(q, kv, kv, torch.zeros(1, 1, dtype=torch.int32),
                                torch.ones(1, dtype=torch.int32), 16, 0.1, 16)
+
+
+def test_device_error_word_encoding():
+    """The device error word's bits and their text (host only): a panel reducer that gives
+    up waiting sets MIQ_DEVERR_PANEL_WAIT (and writes NaN), which check_device_errors
+    turns into a RuntimeError naming it."""
+    from kernels import _lib
+    text = open(HEADER).read()
+    assert re.search(r"MIQ_DEVERR_PANEL_WAIT\s*=\s*1\b", text)
+    assert _lib.device_error_text(0) == "no device error"
+    assert "gave up waiting" in _lib.device_error_text(1)
+    assert "unknown" in _lib.device_error_text(1 << 30)

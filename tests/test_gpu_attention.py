@@ -186,3 +186,33 @@ def test_empty_context_rows(kind):
     live = torch.tensor([1, 3])
     want = A.paged_decode_reference(q[live], k, v, t[live], sl[live], page, D ** -0.5, k_scale=ks, v_scale=vs)
     within(got[live], want)
+
+
+@pytest.mark.parametrize("kind", ["fp8", "int8"])
+def test_config4_full_batch(kind):
+    """BASELINE config 4 at its full size, on the benchmark's own inputs: 64 requests,
+    lengths U[512, 8192] and the shuffled block table from seed 7 (bench.attention_tables),
+    K/V N(0, 1) generated on the device; fp8 with the per-tensor 4/448 scale as a stride-0
+    view, int8 written per (token, kv head) by the HIP quantize-on-write with fp32 scales.
+    Every request of the batch against the oracle, at the default and both benchmarked
+    partitions."""
+    import bench
+    from kernels.paged_attention import paged_decode_attention
+    case(f"config 4 full batch {kind}")
+    a = bench.attention_inputs(torch.device(DEV), kind, copies=1)
+    kc, vc, ks, vs = a["caches"][0]
+    assert a["q"].shape == (64, 32, 128) and a["tokens"] > 200_000
+    if kind == "fp8":
+        assert ks.stride() == (0, 0) and abs(ks[0, 0].item() - 4.0 / 448.0) < 1e-9
+    else:
+        assert ks.dtype == torch.float32 and ks.stride(1) == 1
+    table, lens = a["table"].cpu(), a["lens"].cpu()
+    kcc, vcc = kc.cpu(), vc.cpu()
+    kss = ks[:1, :1].cpu().expand(ks.shape) if kind == "fp8" else ks.cpu()
+    vss = kss if kind == "fp8" else vs.cpu()
+    want = A.paged_decode_reference(a["q"].cpu(), kcc, vcc, table, lens, 16, 128 ** -0.5, k_scale=kss, v_scale=vss)
+    for partition in (None, 256, 512):
+        got = paged_decode_attention(a["q"], kc, vc, a["table"], a["lens"], 16, 128 ** -0.5, a["max_len"],
+                                     k_scale=ks, v_scale=vs, partition=partition)
+        assert rel_error(got, want) < TOL, partition
+        within(got, want)

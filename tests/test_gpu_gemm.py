@@ -80,6 +80,24 @@ def test_w8a16_fp32_scale_and_strided_x():
     within(y, want)
 
 
+@pytest.mark.parametrize("M", [1, 8, 32, 64])
+def test_w8a16_config1_fp32_scales(M):
+    """BASELINE config 1 exactly: fused gate/up N = 19456, K = 2560, fp32 per-row scales
+    (the form bench.py times), every M of the configuration."""
+    from kernels import quant_ops as ops
+    case(f"w8a16 config 1 fp32 scales M={M}")
+    N, K = 19456, 2560
+    w = (torch.randn(N, K, generator=gen(20)) * 0.02)
+    x = make_x(M, K, 21)
+    q = O.int8_quantize(w, torch.float32)
+    assert q["scale"].dtype == torch.float32
+    want = O.int8_linear_fp32(x, **q)
+    y = ops.w8a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV))
+    assert y.dtype == torch.bfloat16 and y.shape == (M, N)
+    within(y, want)
+    assert rel(y, O.int8_linear(x, **q)) < 0.01
+
+
 INT4_SHAPES = [(1, 64, 256, 128), (5, 128, 512, 128), (8, 64, 1024, 256), (16, 192, 384, 128),
                (33, 64, 512, 128), (64, 128, 768, 128), (1, 2560, 9728, 128), (8, 2560, 9728, 128),
                (32, 2560, 9728, 128), (64, 2560, 9728, 128),

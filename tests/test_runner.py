@@ -66,13 +66,25 @@ def olmoe(dtype, seed=0, std=0.05):
 MODELS = {"qwen3": qwen3, "olmoe": olmoe}
 
 
-def cpu_runner(model, kv_dtype=None, pages=64, block=16):
-    from engine.core.model_runner import ModelRunner, PagePool
+def cpu_runner(model, kv_dtype=None, pages=64, block=16, mode="paged", backend="triton"):
+    from engine.core.model_runner import ModelRunner
     a = model.config
     head_dim = getattr(a, "head_dim", None) or a.hidden_size // a.num_attention_heads
     dtype = next(model.parameters()).dtype
-    cache = OracleKVCache(a.num_hidden_layers, a.num_key_value_heads, head_dim, pages * block, dtype, kv_dtype)
-    return ModelRunner(model, cache, decode_attention=oracle_decode_attention), PagePool(pages, block)
+    cache = OracleKVCache(a.num_hidden_layers, a.num_key_value_heads, head_dim, pages * block, dtype, kv_dtype,
+                          mode=mode, block_size=block)
+    return ModelRunner(model, cache, attn_backend=backend, decode_attention=oracle_decode_attention)
+
+
+def teacher_forced_logits(runner, tokens, first):
+    """Logits of every position from `first` on, one prefill over `tokens`."""
+    from engine.core.model_runner import Request
+    req = Request(tokens, 0)
+    runner.cache.admit(req, len(tokens))
+    runner.cache.ensure(req, len(tokens))
+    logits = runner.forward([(req, 0, len(tokens))], all_logits=True)[first:]
+    runner.cache.free(req)
+    return logits
 
 
 def hf_greedy(model, prompt, n):
@@ -87,27 +99,36 @@ def test_runner_matches_transformers_generate(name):
     attention, MLP / MoE, head) reproduces transformers' greedy tokens exactly in fp32."""
     from engine.core.model_runner import generate
     model = MODELS[name](torch.float32)
-    runner, pool = cpu_runner(model)
-    got = generate(runner, pool, PROMPTS[:4], NEW_TOKENS[:4])
+    got = generate(cpu_runner(model), PROMPTS[:4], NEW_TOKENS[:4])
     with torch.no_grad():
         want = [hf_greedy(model, p, n) for p, n in zip(PROMPTS[:4], NEW_TOKENS[:4])]
     assert got == want
+
+
+@pytest.mark.parametrize("mode,backend", [("contiguous", "triton"), ("paged", "sdpa"), ("contiguous", "sdpa")])
+def test_runner_cache_modes_and_backends_agree(mode, backend):
+    """The contiguous cache (page = 1 token-level tables) and the gathered "sdpa" decode
+    backend give the paged kernel path's tokens and logits (reference model_runner.py:
+    139-195 runs either backend over either cache)."""
+    from engine.core.model_runner import generate
+    model = qwen3(torch.float32, seed=2)
+    base_logits, logits = [], []
+    want = generate(cpu_runner(model), PROMPTS, NEW_TOKENS, logits_out=base_logits)
+    got = generate(cpu_runner(model, mode=mode, backend=backend), PROMPTS, NEW_TOKENS, logits_out=logits)
+    assert got == want
+    for a, b in zip(base_logits, logits):
+        assert torch.allclose(torch.stack(a), torch.stack(b), atol=1e-4, rtol=1e-4)
 
 
 def test_oracle_cache_quantized_prefix_is_causal():
     """Teacher forcing one prefill over a sequence gives the logits that token-by-token
     decoding gives, also with an 8-bit cache (each token's codes depend on that token only):
     the identity the GPU parity test relies on."""
-    from engine.core.model_runner import BatchMetadata, Request, generate
+    from engine.core.model_runner import generate
     model = qwen3(torch.float32, seed=1)
-    runner, pool = cpu_runner(model, kv_dtype="int8")
     logits = []
-    out = generate(runner, pool, [PROMPTS[1]], 6, logits_out=logits)[0]
-    runner2, pool2 = cpu_runner(model, kv_dtype="int8")
-    req = Request(0, PROMPTS[1] + out[:-1], 0)
-    pool2.ensure(req, len(req.all_ids))
-    meta = BatchMetadata([(req, 0, len(req.all_ids))], runner2.cache, pool2, "cpu")
-    full = runner2.forward(meta, all_logits=True)[len(PROMPTS[1]) - 1:]
+    out = generate(cpu_runner(model, kv_dtype="int8"), [PROMPTS[1]], 6, logits_out=logits)[0]
+    full = teacher_forced_logits(cpu_runner(model, kv_dtype="int8"), PROMPTS[1] + out[:-1], len(PROMPTS[1]) - 1)
     assert torch.allclose(torch.stack(logits[0]), full, atol=1e-4, rtol=1e-4)
 
 
@@ -120,7 +141,7 @@ GPU_CASES = [("qwen3", "int8_wo", "int8"), ("qwen3", "int4_wo", "fp8"), ("qwen3"
 @pytest.mark.parametrize("name,method,kv", GPU_CASES)
 def test_quantized_greedy_matches_oracle(name, method, kv):
     from engine.core.kv_cache import KVCache
-    from engine.core.model_runner import BatchMetadata, ModelRunner, PagePool, Request, generate
+    from engine.core.model_runner import ModelRunner, generate
     from engine.quantization import get_method
     from engine.quantization.loader import quantize_model
     print(f"[case] greedy parity {name} {method} kv={kv}", flush=True)
@@ -135,7 +156,7 @@ def test_quantized_greedy_matches_oracle(name, method, kv):
                     block_size=block, kv_dtype=kv)
     runner = ModelRunner(model, cache)
     logits = []
-    outs = generate(runner, PagePool(pages, block), PROMPTS, NEW_TOKENS, logits_out=logits)
+    outs = generate(runner, PROMPTS, NEW_TOKENS, logits_out=logits)
     assert [len(o) for o in outs] == NEW_TOKENS
     # the same codes through the bf16 restatement, teacher-forced on the GPU's tokens
     ref = oracle_model(model, torch.bfloat16)
@@ -144,11 +165,7 @@ def test_quantized_greedy_matches_oracle(name, method, kv):
     total = exact = 0
     errs = []
     for i, (prompt, out) in enumerate(zip(PROMPTS, outs)):
-        orunner, opool = cpu_runner(ref, kv_dtype=kv)
-        req = Request(0, prompt + out[:-1], 0)
-        opool.ensure(req, len(req.all_ids))
-        meta = BatchMetadata([(req, 0, len(req.all_ids))], orunner.cache, opool, "cpu")
-        want = orunner.forward(meta, all_logits=True)[len(prompt) - 1:].float()
+        want = teacher_forced_logits(cpu_runner(ref, kv_dtype=kv), prompt + out[:-1], len(prompt) - 1).float()
         got = torch.stack(logits[i])
         errs.append((got - want).abs().flatten())
         top = want.max(dim=-1).values
@@ -166,9 +183,8 @@ def test_quantized_greedy_matches_oracle(name, method, kv):
     # GPU's (reference tests/test_models.py:152-187 compares generated tokens): equal up to
     # the first divergence, and at that step the restatement's own choice must beat the
     # GPU's token by no more than a near-tie (both see the same prefix there)
-    orunner, opool = cpu_runner(ref, kv_dtype=kv)
     ologits = []
-    oouts = generate(orunner, opool, PROMPTS, NEW_TOKENS, logits_out=ologits)
+    oouts = generate(cpu_runner(ref, kv_dtype=kv), PROMPTS, NEW_TOKENS, logits_out=ologits)
     same = 0
     for i, (out, oout) in enumerate(zip(outs, oouts)):
         first = next((j for j, (a, b) in enumerate(zip(out, oout)) if a != b), None)
