@@ -34,6 +34,10 @@ Tuning read_tuning() {
   t.wo_panel_s = ps ? atoi(ps) : 0;
   const char* pm = getenv("MIQ_WO_PANEL_MT");
   t.wo_panel_mt = pm ? atoi(pm) : 0;
+  const char* gv = getenv("MIQ_WO_GEMV_MAX_M");
+  t.wo_gemv_max_m = gv ? atoi(gv) : -1;
+  const char* gw = getenv("MIQ_WO_GEMV_WAVES");
+  t.wo_gemv_waves = gw ? atoi(gw) : 0;
   const char* pmm = getenv("MIQ_WO_PREFILL_MIN_M");
   t.wo_prefill_min_m = pmm && atoi(pmm) > 0 ? atoi(pmm) : 65;
   const char* pps = getenv("MIQ_WO_PREFILL_S");

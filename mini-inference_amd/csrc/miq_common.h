@@ -199,6 +199,8 @@ struct Tuning {
   int wo_panel;               // MIQ_WO_PANEL: 0 off, 1 forced where it applies, -1 default
   int wo_panel_s;             // MIQ_WO_PANEL_S: K splits of the panel kernel (0: planned)
   int wo_panel_mt;            // MIQ_WO_PANEL_MT: activation tiles per panel workgroup (1, 2, 4)
+  int wo_gemv_max_m;          // MIQ_WO_GEMV_MAX_M: largest M for the GEMV kernel (0: off, -1: default 1)
+  int wo_gemv_waves;          // MIQ_WO_GEMV_WAVES: wavefronts per GEMV workgroup (0: planned)
   int wo_prefill_min_m;       // MIQ_WO_PREFILL_MIN_M: smallest M for the prefill kernel (65)
   int wo_prefill_s;           // MIQ_WO_PREFILL_S: K splits of the prefill kernel (0: planned)
   bool fp8_old;               // MIQ_FP8_OLD: the previous FP8 GEMM kernel family

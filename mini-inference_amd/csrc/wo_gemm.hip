@@ -26,6 +26,9 @@ int wo_prefill_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w
                       const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int64_t M,
                       int N, int K, void* workspace, size_t ws_bytes, size_t counter_bytes, hipStream_t st,
                       const char* name);
+int wo_gemv_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, const void* scale,
+                   const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int M,
+                   int N, int K, hipStream_t st, const char* name, bool& launched);
 size_t wo_tile_pair_bytes(int64_t M, int64_t N);
 int wo_tile_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, const void* scale,
                    const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int M,
@@ -62,6 +65,11 @@ int run(int kind, const WoArgs& p, void* workspace, size_t ws_bytes, hipStream_t
     return wo_prefill_launch(kind, p.x, p.ldx, p.w, p.ldw, p.scale, p.zero, p.sz_dtype, p.group_steps, p.ngroups,
                              p.y, p.ldy, p.M, p.N, p.K, workspace, ws_bytes, kWoCounterBytes, st, name);
   bool launched = false;
+  {
+    const int rc = wo_gemv_launch(kind, p.x, p.ldx, p.w, p.ldw, p.scale, p.zero, p.sz_dtype, p.group_steps,
+                                  p.ngroups, p.y, p.ldy, p.M, p.N, p.K, st, name, launched);
+    if (launched || rc != MIQ_OK) return rc;
+  }
   if (kind == KIND_INT4) {
     const int rc = wo_panel_launch(p.x, p.ldx, p.w, p.ldw, p.scale, p.zero, p.sz_dtype, p.group_steps, p.ngroups,
                                    p.y, p.ldy, p.M, p.N, p.K, workspace, ws_bytes, kWoCounterBytes, st, name,

@@ -112,7 +112,7 @@ PLANS = {"default": {}, "panel": {"MIQ_WO_PANEL": "1"},
          "panel_s16": {"MIQ_WO_PANEL": "1", "MIQ_WO_PANEL_S": "16"},
          "panel_mt2": {"MIQ_WO_PANEL": "1", "MIQ_WO_PANEL_MT": "2"},
          "panel_mt4": {"MIQ_WO_PANEL": "1", "MIQ_WO_PANEL_MT": "4"},
-         "nopanel": {"MIQ_WO_PANEL": "0"},
+         "nopanel": {"MIQ_WO_PANEL": "0"}, "tile_m1": {"MIQ_WO_GEMV_MAX_M": "0"},
          "msplit_4_3": {"MIQ_WO_PANEL": "0"}, "msplit_off": {"MIQ_WO_PANEL": "0"}}
 
 
@@ -173,10 +173,14 @@ TILE_CASES = [(1, 320, 9728, 128), (4, 320, 9728, 128), (3, 160, 1152, 128), (2,
 # kernel, the streamed kernel, the tile kernel with a forced number of weight rows per
 # tile (16, and 7: a tile whose 128-byte loads are partly empty) on one workgroup per tile,
 # and the two-half plan forced from one row on
-KERNELS = {"auto": {}, "nopanel": {"MIQ_WO_PANEL": "0"}, "stream": {"MIQ_WO_STREAM": "1"},
-           "rows16": {"MIQ_WO_ROWS": "16", "MIQ_WO_PANEL": "0", "MIQ_WO_PAIR_MIN_M": "-1"},
-           "rows7": {"MIQ_WO_ROWS": "7", "MIQ_WO_PANEL": "0", "MIQ_WO_PAIR_MIN_M": "-1"},
-           "pair": {"MIQ_WO_PANEL": "0", "MIQ_WO_PAIR_MIN_M": "1"}}
+# The GEMV kernel (M = 1 by default) is switched off in the plans that test the tile
+# kernel, and forced up to M = 2 in "gemv2".
+_NOGEMV = {"MIQ_WO_GEMV_MAX_M": "0"}
+KERNELS = {"auto": {}, "gemv2": {"MIQ_WO_GEMV_MAX_M": "2"}, "nopanel": {"MIQ_WO_PANEL": "0", **_NOGEMV},
+           "stream": {"MIQ_WO_STREAM": "1"},
+           "rows16": {"MIQ_WO_ROWS": "16", "MIQ_WO_PANEL": "0", "MIQ_WO_PAIR_MIN_M": "-1", **_NOGEMV},
+           "rows7": {"MIQ_WO_ROWS": "7", "MIQ_WO_PANEL": "0", "MIQ_WO_PAIR_MIN_M": "-1", **_NOGEMV},
+           "pair": {"MIQ_WO_PANEL": "0", "MIQ_WO_PAIR_MIN_M": "1", **_NOGEMV}}
 
 
 @pytest.mark.parametrize("kernel", list(KERNELS))
@@ -202,7 +206,8 @@ def test_w4a16_tile_and_stream(kernel, M, N, K, group, sdt, symmetric, miq_env):
 # int8 kernels: as above, plus workgroups of two row tiles over all of K (at 4 and 5 rows by
 # default, forced from one row): N an odd number of 16-row tiles (2512, 1008), K = 4096
 # (eight wavefronts of 4 k-steps, the most that plan holds)
-KERNELS8 = dict(KERNELS, tile2={"MIQ_WO_INT8_TILE2_MIN_M": "1"}, one_tile={"MIQ_WO_INT8_TILE2_MIN_M": "-1"})
+KERNELS8 = dict(KERNELS, tile2={"MIQ_WO_INT8_TILE2_MIN_M": "1", **_NOGEMV},
+                one_tile={"MIQ_WO_INT8_TILE2_MIN_M": "-1", **_NOGEMV})
 
 
 @pytest.mark.parametrize("kernel", list(KERNELS8))
