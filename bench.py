@@ -86,6 +86,43 @@ def time_graph(fn_list, reps=1):
     return start.elapsed_time(end) / 1e3 / reps
 
 
+_FLOOR_CACHE = {}
+
+
+def stream_floor_us(nbytes, dev):
+    """Time of a plain streaming read of `nbytes` (miq_stream_read: 16-byte non-temporal
+    loads over 2048 workgroups), the same graph timing as the kernels, each read from a
+    window of a buffer of at least 640 MiB that the previous reads did not touch (MALL
+    defeated). The floor a launch of that many bytes can reach on this GPU."""
+    from kernels import _lib
+    nbytes = int(nbytes) // 16 * 16
+    if nbytes in _FLOOR_CACHE:
+        return _FLOOR_CACHE[nbytes]
+    total = max(640 << 20, 3 * nbytes)
+    buf = torch.empty(total, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    lib = _lib.load()
+    nwin = max(2, (total - nbytes) // max(nbytes, 1 << 20))
+    step = ((total - nbytes) // nwin) // 4096 * 4096
+    def rd(i):  # the stream is looked up at call time: under capture it is the capture stream
+        off = (i % (nwin + 1)) * step
+        return lambda: lib.miq_stream_read(buf.data_ptr() + off, nbytes, sink.data_ptr(),
+                                           torch.cuda.current_stream(dev).cuda_stream)
+    reps = 20
+    t = min(time_graph([rd(i) for i in range(reps)]) / reps for _ in range(2))
+    del buf
+    _FLOOR_CACHE[nbytes] = round(t * 1e6, 2)
+    return _FLOOR_CACHE[nbytes]
+
+
+def with_floor(entry, nbytes, dev):
+    """Adds the streaming-read floor of `nbytes` to a timing entry that has "us"."""
+    f = stream_floor_us(nbytes, dev)
+    entry["stream_floor_us"] = f
+    entry["frac_of_stream_floor"] = round(f / entry["us"], 3)
+    return entry
+
+
 def host_cpu():
     try:
         for line in open("/proc/cpuinfo"):
@@ -152,7 +189,8 @@ def per_m(cfg, launch, nbytes, dev, reps_per_graph=40, ref_launch=None):
     for M in MS:
         t = time_graph([launch(cfg, M, i) for i in range(reps_per_graph)]) / reps_per_graph
         gbs = nbytes(cfg, M) / t / 1e9
-        out[f"M={M}"] = {"us": round(t * 1e6, 2), "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1)}
+        out[f"M={M}"] = with_floor({"us": round(t * 1e6, 2), "GB/s": round(gbs, 1),
+                                    "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1)}, nbytes(cfg, M), dev)
         if ref_launch is not None:
             n = 8
             tr = time_graph([ref_launch(cfg, M, i) for i in range(n)]) / n
@@ -287,8 +325,11 @@ def bench_attention(dev, kind):
     for partition in (256, 512):
         t = time_graph([call(i, partition) for i in range(reps)]) / reps
         gbs = a["bytes"] / t / 1e9
-        res[f"partition_{partition}"] = {"us_per_step": round(t * 1e6, 2), "GB/s": round(gbs, 1),
-                                         "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1)}
+        e = {"us_per_step": round(t * 1e6, 2), "GB/s": round(gbs, 1),
+             "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1)}
+        e["stream_floor_us"] = stream_floor_us(a["bytes"], dev)
+        e["frac_of_stream_floor"] = round(e["stream_floor_us"] / e["us_per_step"], 3)
+        res[f"partition_{partition}"] = e
     from kernels.paged_attention.decode import choose_partition
     kc = a["caches"][0][0]
     res["default_partition"] = choose_partition(a["max_len"], None, kc.dtype)
@@ -343,6 +384,8 @@ def bench_moe(dev):
     res = {"us_per_layer": round(t * 1e6, 2), "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
            "experts_touched": c["touched"], "MB_per_call": round(c["bytes"] / 1e6, 1),
            "grouped_per_expert_path_us": round(tg * 1e6, 1)}
+    res["stream_floor_us"] = stream_floor_us(c["bytes"], dev)
+    res["frac_of_stream_floor"] = round(res["stream_floor_us"] / res["us_per_layer"], 3)
     del c
     return res
 
@@ -376,9 +419,11 @@ def bench_moe_int8(dev):
     gq, gs, dq, ds = sets[0]
     tg = grouped_path_time(Int8WeightOnly(), E, {"qweight": gq, "scale": gs}, {"qweight": dq, "scale": ds},
                            hidden, idx, w)
+    floor = stream_floor_us(nbytes, dev)
     return {"us_per_layer": round(t * 1e6, 2), "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
             "experts_touched": touched, "MB_per_call": round(nbytes / 1e6, 1),
-            "grouped_per_expert_path_us": round(tg * 1e6, 1)}
+            "grouped_per_expert_path_us": round(tg * 1e6, 1), "stream_floor_us": floor,
+            "frac_of_stream_floor": round(floor / (t * 1e6), 3)}
 
 
 def grouped_path_time(method, E, gate_up, down, hidden, idx, w, reps=5):
@@ -432,9 +477,11 @@ def bench_moe_fp8(dev):
     gq, gs, dq, ds = sets[0]
     tg = grouped_path_time(FP8WeightAct(device=dev), E, {"qweight": gq, "scale": gs}, {"qweight": dq, "scale": ds},
                            hidden, idx, w)
+    floor = stream_floor_us(nbytes, dev)
     return {"us_per_layer": round(t * 1e6, 2), "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1),
             "experts_touched": touched, "MB_per_call": round(nbytes / 1e6, 1),
-            "grouped_per_expert_path_us": round(tg * 1e6, 1)}
+            "grouped_per_expert_path_us": round(tg * 1e6, 1), "stream_floor_us": floor,
+            "frac_of_stream_floor": round(floor / (t * 1e6), 3)}
 
 
 # ---------------------------------------------------------------- CPU baselines (oracle)
@@ -675,8 +722,10 @@ def main():
 
     log("[bench] headline: INT4 W4A16 decode GEMM sweep")
     cfg, step_bytes, t = bench_headline(dev, args.steps, args.warmup)
+    launch_bytes = [int4_bytes(cfg, M) for M in MS]
     del cfg
     torch.cuda.empty_cache()
+    floor_step_us = round(sum(stream_floor_us(nb, dev) for nb in launch_bytes), 2)
     ms_per_step = t / args.steps * 1e3
     value = step_bytes * args.steps / t / 1e9
     avg_kernel_us = t / (4 * args.steps) * 1e6
@@ -710,8 +759,12 @@ def main():
                 "traffic": traffic["bytes_per_launch"] if traffic else None,
                 "traffic_unit": "bytes per launch (HBM, rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)",
                 "algorithmic_bytes_per_launch": round(step_bytes / 4),
-                "kernel": "wo_tile_kernel<int4> (M=1, 8) and wo_panel_kernel<int4> (M=32, 64)",
-                "avg_kernel_us": round(avg_kernel_us, 3)}
+                "kernel": "wo_gemv_kernel<int4> (M=1), wo_tile_kernel<int4> (M=8) and wo_panel_kernel<int4> (M=32, 64)",
+                "avg_kernel_us": round(avg_kernel_us, 3),
+                "stream_floor_us_per_step": floor_step_us,
+                "frac_of_stream_floor": round(floor_step_us / (t / args.steps * 1e6), 3),
+                "stream_floor_note": "miq_stream_read of each launch's algorithmic bytes, same graph timing; "
+                                     "includes the per-launch cost a graph node has on this GPU"}
     if traffic:
         roofline["traffic_per_M"] = traffic["per_M_bytes"]
         roofline["traffic_calibration"] = {"fetch_scale": traffic["fetch_scale"], "write_scale": traffic["write_scale"]}

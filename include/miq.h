@@ -2,10 +2,11 @@
  *
  * C ABI only: raw device pointers, element counts/strides in elements (int64), a dtype
  * enum for operands whose type varies, and the HIP stream to launch on (passed as
- * void* so this header needs no HIP include). No function allocates device memory,
- * synchronises the host, or keeps state between calls, with one exception: the
- * split-K counters inside a caller-provided workspace are left at zero by every call
- * (the caller zeroes the workspace once when it allocates it).
+ * void* so this header needs no HIP include). No function allocates device memory or
+ * keeps state between calls, and only miq_device_errors synchronises the host. The one
+ * exception to "no state": the split-K counters and exchange words inside a
+ * caller-provided workspace are left at zero by every call (the caller zeroes the
+ * workspace once when it allocates it).
  *
  * Every function returns MIQ_OK (0) or a negative MIQ_ERR_* code; miq_last_error()
  * returns a thread-local message for the last failure.
@@ -57,6 +58,11 @@ int miq_device_errors(unsigned* bits, void* stream);
 
 /* Text for error word `bits` (host only, needs no GPU). */
 const char* miq_device_error_string(unsigned bits);
+
+/* Reads `bytes` bytes (a multiple of 16) of `buf` as a plain stream: the HBM streaming
+ * floor a benchmark sets kernel times against. No counterpart in the reference (a
+ * measurement helper); `sink` is a device int that is practically never written. */
+int miq_stream_read(const void* buf, size_t bytes, int* sink, void* stream);
 
 /* Re-reads the MIQ_* kernel-selection variables (MIQ_WO_STREAM, MIQ_WO_PANEL, ...), which
  * the library otherwise reads once when it is loaded. No counterpart in the reference: a

@@ -135,3 +135,29 @@ extern "C" int miq_tuning_reload(void) {
   miq::g_tuning = miq::read_tuning();
   return MIQ_OK;
 }
+
+// ------------------------------------------------------------------ streaming-read floor
+// A plain read of `bytes` bytes (16-byte non-temporal loads, grid-stride, 2048 workgroups of
+// 256 threads: the fastest of the shapes measured on MI355X for 12-50 MB), so that a kernel's
+// time can be set against the time the same number of bytes takes to stream from HBM.
+namespace miq {
+namespace {
+__global__ void __launch_bounds__(256) stream_read_kernel(const i32x4* __restrict__ p, int64_t n16, int* sink) {
+  int acc = 0;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n16; i += stride) {
+    const i32x4 v = __builtin_nontemporal_load(p + i);
+    acc ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+  if (acc == 0x5eed1234) sink[0] = acc;  // keeps the loads; practically never stored
+}
+}  // namespace
+}  // namespace miq
+
+extern "C" int miq_stream_read(const void* buf, size_t bytes, int* sink, void* stream) {
+  MIQ_REQUIRE(buf != nullptr && sink != nullptr && (reinterpret_cast<uintptr_t>(buf) & 15) == 0,
+              "stream_read: buf must be 16-byte aligned and sink non-NULL");
+  hipLaunchKernelGGL(miq::stream_read_kernel, dim3(2048), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const miq::i32x4*>(buf), (int64_t)(bytes / 16), sink);
+  return miq::check_launch("stream_read");
+}

@@ -38,6 +38,7 @@ SIGNATURES = {
     "miq_tuning_reload": (_I32, []),
     "miq_device_errors": (_I32, [_P, _P]),
     "miq_device_error_string": (ctypes.c_char_p, [ctypes.c_uint]),
+    "miq_stream_read": (_I32, [_P, _SZ, _P, _P]),
     "miq_int8_quantize": (_I32, [_P, _I32, _I64, _I64, _I64, _P, _P, _I32, _P]),
     "miq_int8_dequantize": (_I32, [_P, _P, _I32, _I64, _I64, _P, _P]),
     "miq_int4_quantize": (_I32, [_P, _I32, _I64, _I64, _I64, _I64, _P, _P, _P, _I32, _P]),
