@@ -17,9 +17,10 @@
 //     into the order in which the codes unpack), and each piece is multiplied as soon as
 //     its own load has arrived (loads complete in order).
 // A piece is 32 int4 or 16 int8 codes of one row, inside one quantization group. Codes
-// become bf16 128 + code (int4: one AND-OR per pair of codes, int8: xor 0x80 and a byte
-// convert), multiplied with v_dot2c_f32_bf16 against the staged activations in fp32, and
-// the 128 offset is removed with the piece's activation sum (staged with the rows). At
+// become bf16 values (int4: 128 + code, one AND-OR per pair of codes; int8: the signed
+// code, one sign-extending byte convert per code), multiplied with v_dot2c_f32_bf16
+// against the staged activations in fp32; for int4 the 128 offset is removed with the
+// piece's activation sum (staged with the rows). At
 // M = 1 the multiply, not the loads, sets the time beyond the streaming read (MI355X,
 // N = 2560, K = 9728: 3.7 us with the loads alone, 4.9 us with the multiply alone, 5.6 us
 // together), so the address arithmetic is division-free and every wavefront keeps four
@@ -28,7 +29,7 @@
 // measured slower (5.95 us): each round waits on a chain of four MFMAs.
 //   int4  acc += s_g * (sum x (128 + u) + bias * sum x) [+ z_g * sum x]
 //         (bias -136 for symmetric codes, -128 with zero points)
-//   int8  y = bf16(bf16(sum x (128 + q) - 128 sum x) * bf16(s))   (int8_wo.py:17-21)
+//   int8  y = bf16(bf16(sum x q) * bf16(s))                       (int8_wo.py:17-21)
 // The lanes' partial sums of a row are added by a fixed DPP tree, so results are
 // deterministic; there is no workspace and no cross-workgroup exchange.
 #include <algorithm>
@@ -76,6 +77,15 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 __device__ inline float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+// 4 signed int8 codes -> 2 dwords of bf16 pairs (exact: |q| <= 128 has at most 8
+// significant bits); the byte selects become SDWA sign-extending converts
+__device__ inline void s8x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  const float f0 = (float)(int8_t)(w & 0xff), f1 = (float)(int8_t)((w >> 8) & 0xff);
+  const float f2 = (float)(int8_t)((w >> 16) & 0xff), f3 = (float)(int8_t)(w >> 24);
+  lo = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0), 0x07060302u);
+  hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f3), __builtin_bit_cast(uint32_t, f2), 0x07060302u);
 }
 
 template <int CTRL>
@@ -200,16 +210,19 @@ wo_gemv_kernel(GemvParams p) {
     const int i = tid + t * nthreads;
     const int m = i >= p8 ? 1 : 0, c8 = i - m * p8;
     const uint4 v = xv[t];
-    float s8 = dot2(v.x, 0x3f803f80u, 0.f);
-    s8 = dot2(v.y, 0x3f803f80u, s8);
-    s8 = dot2(v.z, 0x3f803f80u, s8);
-    s8 = dot2(v.w, 0x3f803f80u, s8);
-    s8 = dpp_add<0xB1>(s8);                    // pairs of threads (16 k)
-    if constexpr (I4) s8 = dpp_add<0x4E>(s8);  // quads (32 k)
+    float s8 = 0.f;
+    if constexpr (I4) {
+      s8 = dot2(v.x, 0x3f803f80u, 0.f);
+      s8 = dot2(v.y, 0x3f803f80u, s8);
+      s8 = dot2(v.z, 0x3f803f80u, s8);
+      s8 = dot2(v.w, 0x3f803f80u, s8);
+      s8 = dpp_add<0xB1>(s8);  // pairs of threads (16 k)
+      s8 = dpp_add<0x4E>(s8);  // quads (32 k)
+    }
     if (i < M * p8) {
       const int pc = c8 / kChunks, e = c8 - pc * kChunks;
       *reinterpret_cast<uint4*>(xl + m * (K / 2) + (e * npc + pc) * 4) = I4 ? permute_for_u4(v) : v;
-      if (e == 0) xs[m * npc + pc] = s8;
+      if (I4 && e == 0) xs[m * npc + pc] = s8;
     }
   }
   __syncthreads();
@@ -252,19 +265,21 @@ wo_gemv_kernel(GemvParams p) {
           de[e] = dot2(((w >> 12) & mk) | ob, xq.w, de[e]);
         }
       } else {
+        // int8: the signed codes themselves (no 128 offset, so no activation sums)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
           const uint4 xq = *reinterpret_cast<const uint4*>(xr + h * npc * 4);
           uint32_t lo, hi;
-          unpack_i8_word(wd[2 * h], lo, hi);
-          de[2 * h] = dot2(lo, xq.x, 0.f);
-          de[2 * h] = dot2(hi, xq.y, de[2 * h]);
-          unpack_i8_word(wd[2 * h + 1], lo, hi);
-          de[2 * h + 1] = dot2(lo, xq.z, 0.f);
-          de[2 * h + 1] = dot2(hi, xq.w, de[2 * h + 1]);
+          s8x4_to_bf16(wd[2 * h], lo, hi);
+          de[h] = dot2(lo, xq.x, 0.f);
+          de[h] = dot2(hi, xq.y, de[h]);
+          s8x4_to_bf16(wd[2 * h + 1], lo, hi);
+          de[h] = dot2(lo, xq.z, de[h]);
+          de[h] = dot2(hi, xq.w, de[h]);
         }
+        de[2] = de[3] = 0.f;
       }
-      const float d = (de[0] + de[1]) + (de[2] + de[3]);
+      const float d = I4 ? (de[0] + de[1]) + (de[2] + de[3]) : de[0] + de[1];
       float t;
       if constexpr (I4) {
         const float xsum = xs[m * npc + c];
@@ -276,15 +291,6 @@ wo_gemv_kernel(GemvParams p) {
       t = live ? t : 0.f;
       acc[m][0] += pslot[i] ? 0.f : t;  // selects, not branches
       acc[m][1] += pslot[i] ? t : 0.f;
-    }
-  }
-  float xtot[MR];
-#pragma unroll
-  for (int m = 0; m < MR; ++m) {
-    xtot[m] = 0.f;
-    if (!I4 && m < M) {  // int8: the whole row's activation sum (every row uses all of K)
-      for (int c = lane; c < npc; c += 64) xtot[m] += xs[m * npc + c];
-      xtot[m] = wave_sum(xtot[m]);
     }
   }
 
@@ -299,7 +305,7 @@ wo_gemv_kernel(GemvParams p) {
       const float tot = wave_sum(acc[m][rr]);
       if (lane == 0 && row < p.N) {
         if constexpr (!I4) {
-          const float a = bf16_to_f32(f32_to_bf16(__builtin_fmaf(-128.f, xtot[m], tot)));
+          const float a = bf16_to_f32(f32_to_bf16(tot));
           const float s = bf16_to_f32(f32_to_bf16(sd_to_f32<SD>(rsc[rr])));
           p.y[(int64_t)m * p.ldy + row] = f32_to_bf16(a * s);
         } else {
