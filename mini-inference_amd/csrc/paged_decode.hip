@@ -465,6 +465,10 @@ paged_decode_split8_kernel(AttnParams p) {
   uint8_t* vl = s_v[wv];
   uint16_t* pp = s_p[wv];
   const int tq = (lane >> 3) * 4, dseg = (lane & 7) * 16;  // V: 4 tokens x 16 d per lane
+  // V load i of a 32-token step covers, per lane, token vtok(i) of the step: with
+  // 16-token pages, tokens 8 i + lane / 8 (so each load lies in one page and is addressed
+  // from that page's base), else tokens tq + i
+  auto vtok = [&](int i) { return P16 ? 8 * i + (lane >> 3) : tq + i; };
   const int pshift = p.page_shift, page = p.page;
   // NC > 0: the block-table entries of the partition are staged in LDS once per
   // workgroup, so slot lookups are LDS reads instead of global loads that would queue
@@ -518,21 +522,17 @@ paged_decode_split8_kernel(AttnParams p) {
   const int bp_addr = (32 * (r >> 3) + 4 * (r & 7) + g) * 4;
   KLoadSlots kls;
   // chunk ci of the wavefront starts at token c0 (ci is a compile-time index where P16 uses it)
-  auto lookup = [&](int c0, int ci, KSlots& ks, VSlots& vs) {  // K / P tokens c0 + 32 s + 16 c + r, V tokens c0 + 32 s + tq + i
+  // P16: the page of each 16 tokens of the chunk (uniform: scalar registers)
+  int cpg[kPagesPerChunk > 0 ? CS * 2 : 1];
+  auto lookup = [&](int c0, int ci, KSlots& ks, VSlots& vs) {  // K / P tokens c0 + 32 s + 16 c + r, V tokens c0 + 32 s + vtok(i)
     if constexpr (P16) {
 #pragma unroll
       for (int s = 0; s < CS; ++s) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
           const int pg = wpage[ci * kPagesPerChunk + 2 * s + c];
+          cpg[2 * s + c] = pg;
           ks[s][c] = pg * 16 + r;
-#pragma unroll
-          for (int h = 0; h < 2; ++h) kls[s][c][h] = pg * 16 + 8 * h + lrr;
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int tt = tq + i;
-          vs[s][i] = (tt < 16 ? wpage[ci * kPagesPerChunk + 2 * s] : wpage[ci * kPagesPerChunk + 2 * s + 1]) * 16 + (tt & 15);
         }
       }
       return;
@@ -552,14 +552,31 @@ paged_decode_split8_kernel(AttnParams p) {
   constexpr int NB = NC > 1 ? 2 : 1;  // register sets (chunk c + 1 loads while chunk c computes)
   uint4 kr[NB][CS][2][2], vr[NB][CS][4];
   uint32_t ksr[NB][CS][2], vsr[NB][CS][2];
+  // P16: a page's 16 token rows are addressed from a buffer descriptor on the page's base
+  // (built in scalar registers from the page id), so each load's lane offset is a constant
+  // and no 64-bit address arithmetic runs per load
+  const int page_bytes = 16 * (int)p.kvs_t;
+  auto page_rsrc = [&](const uint8_t* base, int pg) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base + (int64_t)pg * page_bytes + head_off), 0,
+                                             page_bytes, 0x00020000);
+  };
   auto issue_k = [&](int bi, const KSlots& ks) {
 #pragma unroll
     for (int s = 0; s < CS; ++s)
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
+        if constexpr (P16) {
+          const __amdgpu_buffer_rsrc_t rs = page_rsrc(p.k, cpg[2 * s + c]);
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
-          kr[bi][s][c][h] = load_nt16(p.k + (int64_t)kls[s][c][h] * p.kvs_t + head_off + kchunk);
+          for (int h = 0; h < 2; ++h) {
+            const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, (8 * h + lrr) * (int)p.kvs_t + kchunk, 0, 2 /* nt */);
+            kr[bi][s][c][h] = *reinterpret_cast<const uint4*>(&v);
+          }
+        } else {
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            kr[bi][s][c][h] = load_nt16(p.k + (int64_t)kls[s][c][h] * p.kvs_t + head_off + kchunk);
+        }
         if (HAS_SCALE) ksr[bi][s][c] = load_sd_raw<SD>(p.ks, (int64_t)ks[s][c] * p.ss_t + (int64_t)kvh * p.ss_h);
       }
   };
@@ -567,8 +584,18 @@ paged_decode_split8_kernel(AttnParams p) {
   auto issue_v = [&](int bi, const KSlots& ks, const VSlots& vs) {
 #pragma unroll
     for (int s = 0; s < CS; ++s) {
+      if constexpr (P16) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vr[bi][s][i] = load_nt16(p.v + (int64_t)vs[s][i] * p.kvs_t + head_off + dseg);
+        for (int i = 0; i < 4; ++i) {
+          const __amdgpu_buffer_rsrc_t rs = page_rsrc(p.v, cpg[2 * s + (i >> 1)]);
+          const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, ((8 * i) & 15 | (lane >> 3)) * (int)p.kvs_t + dseg, 0,
+                                                               2 /* nt */);
+          vr[bi][s][i] = *reinterpret_cast<const uint4*>(&v);
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vr[bi][s][i] = load_nt16(p.v + (int64_t)vs[s][i] * p.kvs_t + head_off + dseg);
+      }
       if (HAS_SCALE) {
 #pragma unroll
         for (int c = 0; c < 2; ++c) vsr[bi][s][c] = load_sd_raw<SD>(p.vs, (int64_t)ks[s][c] * p.ss_t + (int64_t)kvh * p.ss_h);
@@ -650,8 +677,8 @@ paged_decode_split8_kernel(AttnParams p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         uint4 v = vr[bi][s][i];
-        if (partial && c0 + s * kStep + tq + i >= t_end) v = make_uint4(0, 0, 0, 0);  // 0 * NaN is NaN
-        *reinterpret_cast<uint4*>(vl + (s * kStep + tq + i) * kVRowB + dseg) = v;
+        if (partial && c0 + s * kStep + vtok(i) >= t_end) v = make_uint4(0, 0, 0, 0);  // 0 * NaN is NaN
+        *reinterpret_cast<uint4*>(vl + (s * kStep + vtok(i)) * kVRowB + dseg) = v;
       }
     }
     wave_lds_sync();

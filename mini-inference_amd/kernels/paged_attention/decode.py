@@ -4,7 +4,7 @@
 Differences in mechanism, not in results:
   * one workgroup handles all query heads of a kv head (the K/V bytes are read once);
   * the context of each request is cut into fixed partitions of `partition` tokens
-    (multiple of 128; by default 512 for an FP8 cache, 256 otherwise) instead of a
+    (multiple of 128; 256 by default) instead of a
     per-request count of splits. Passing
     num_splits keeps the reference's meaning of "about that many pieces for the longest
     request": the partition becomes cdiv(max_len, num_splits) rounded up to 128.
@@ -19,10 +19,11 @@ import torch
 from kernels import _lib as L
 
 # Default partitions by cache dtype. Config 4 on MI355X (B = 64, 271.5k context tokens),
-# 256 against 512 tokens in the same runs: FP8 143.7 / 145.7 / 146.6-150.6 against 143.5 /
-# 144.1 / 140.1-142.9 us per step; INT8 151 against 161 us
+# with the K / V pages addressed from scalar page bases: FP8 128 / 256 / 512 / 1024 took
+# 141.5 / 135.1 / 137.9 / 139.8 us per step, INT8 149.1 / 145.2 / 156.0 / 161.2 us (one
+# run each, same box)
 DEFAULT_PARTITION = 256
-_DEFAULT_PARTITION_BY_DTYPE = {torch.float8_e4m3fn: 512}
+_DEFAULT_PARTITION_BY_DTYPE = {}
 _KV_DTYPES = (torch.bfloat16, torch.float8_e4m3fn, torch.int8)
 
 
