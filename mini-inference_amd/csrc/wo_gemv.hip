@@ -107,7 +107,7 @@ __device__ inline float wave_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
-constexpr int kGvXPieces = 2;  // 16-byte activation pieces per thread (M * K / 8 <= 2 * threads)
+constexpr int kGvXPR = 2;  // 16-byte activation pieces per thread and activation row (K / 8 <= 2 * threads)
 
 template <int KIND, bool HZ, int SD, int MR>
 __global__ void __launch_bounds__(kGvMaxWaves * 64)
@@ -134,16 +134,17 @@ wo_gemv_kernel(GemvParams p) {
   const int p8 = K / 8;  // 16-byte activation pieces per row
   const __amdgpu_buffer_rsrc_t xrs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(p.x), 0, p.xbytes, 0x00020000);
-  uint4 xv[kGvXPieces];
+  uint4 xv[MR][kGvXPR];
 #pragma unroll
-  for (int t = 0; t < kGvXPieces; ++t) {
-    const int i = tid + t * nthreads;
-    const int m = i >= p8 ? 1 : 0, c = i - m * p8;  // M <= 2 (host plan): no division
-    int off = i < M * p8 && !(kGvAbl & 2) ? (m * p.ldx32 + c * 8) * 2 : kOut;
-    asm volatile("" : "+v"(off));
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
-    xv[t] = *reinterpret_cast<const uint4*>(&v);
-  }
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int t = 0; t < kGvXPR; ++t) {
+      const int c = tid + t * nthreads;
+      int off = m < M && c < p8 && !(kGvAbl & 2) ? (m * p.ldx32 + c * 8) * 2 : kOut;
+      asm volatile("" : "+v"(off));
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
+      xv[m][t] = *reinterpret_cast<const uint4*>(&v);
+    }
 
   // ---- 2. every weight and scale load of the wavefront: lane l takes pieces l, l + 64,
   // ... of the wavefront's range, so each load instruction covers 1 KiB of contiguous
@@ -206,25 +207,26 @@ wo_gemv_kernel(GemvParams p) {
   uint32_t* xl = lds32;                                          // [M][K / 2] dwords
   float* xs = reinterpret_cast<float*>(lds32 + MR * (K / 2));   // [M][npc]
 #pragma unroll
-  for (int t = 0; t < kGvXPieces; ++t) {
-    const int i = tid + t * nthreads;
-    const int m = i >= p8 ? 1 : 0, c8 = i - m * p8;
-    const uint4 v = xv[t];
-    float s8 = 0.f;
-    if constexpr (I4) {
-      s8 = dot2(v.x, 0x3f803f80u, 0.f);
-      s8 = dot2(v.y, 0x3f803f80u, s8);
-      s8 = dot2(v.z, 0x3f803f80u, s8);
-      s8 = dot2(v.w, 0x3f803f80u, s8);
-      s8 = dpp_add<0xB1>(s8);  // pairs of threads (16 k)
-      s8 = dpp_add<0x4E>(s8);  // quads (32 k)
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int t = 0; t < kGvXPR; ++t) {
+      const int c8 = tid + t * nthreads;
+      const uint4 v = xv[m][t];
+      float s8 = 0.f;
+      if constexpr (I4) {
+        s8 = dot2(v.x, 0x3f803f80u, 0.f);
+        s8 = dot2(v.y, 0x3f803f80u, s8);
+        s8 = dot2(v.z, 0x3f803f80u, s8);
+        s8 = dot2(v.w, 0x3f803f80u, s8);
+        s8 = dpp_add<0xB1>(s8);  // pairs of threads (16 k)
+        s8 = dpp_add<0x4E>(s8);  // quads (32 k)
+      }
+      if (m < M && c8 < p8) {
+        const int pc = c8 / kChunks, e = c8 - pc * kChunks;
+        *reinterpret_cast<uint4*>(xl + m * (K / 2) + (e * npc + pc) * 4) = I4 ? permute_for_u4(v) : v;
+        if (I4 && e == 0) xs[m * npc + pc] = s8;
+      }
     }
-    if (i < M * p8) {
-      const int pc = c8 / kChunks, e = c8 - pc * kChunks;
-      *reinterpret_cast<uint4*>(xl + m * (K / 2) + (e * npc + pc) * 4) = I4 ? permute_for_u4(v) : v;
-      if (I4 && e == 0) xs[m * npc + pc] = s8;
-    }
-  }
   __syncthreads();
 
   if constexpr ((kGvAbl & 1) != 0) {  // probe: consume the loads without the multiply
@@ -329,9 +331,15 @@ void launch_gemv(const GemvParams& p, unsigned grid, unsigned threads, size_t ld
   hipLaunchKernelGGL((wo_gemv_kernel<KIND, HZ, SD, MR>), dim3(grid), dim3(threads), lds, st, p);
 }
 
+// activation rows of the kernel instance that takes M rows. Instances for 4 and 8 rows
+// measured slower than the tile and streamed kernels on MI355X (INT8 N = 19456, K = 2560:
+// M = 4 / 8 17.4 / 33.5 against 13.1 / 15.5 us; INT4 N = 2560, K = 9728, M = 4: 7.8 us with
+// 8-wavefront workgroups against 8.1), so at most 2 rows are built
+constexpr int gemv_rows(int64_t M) { return M <= 1 ? 1 : 2; }
+
 template <int KIND, bool HZ, int SD>
 void launch_m(int M, const GemvParams& p, unsigned grid, unsigned threads, size_t lds, hipStream_t st) {
-  if (M == 1) launch_gemv<KIND, HZ, SD, 1>(p, grid, threads, lds, st);
+  if (gemv_rows(M) == 1) launch_gemv<KIND, HZ, SD, 1>(p, grid, threads, lds, st);
   else launch_gemv<KIND, HZ, SD, 2>(p, grid, threads, lds, st);
 }
 
@@ -362,8 +370,8 @@ GemvPlan plan_gemv(int kind, int64_t M, int64_t N, int64_t K) {
   int W = kind == KIND_INT8 ? 4 : (int)std::min<int64_t>(kGvMaxWaves, std::max<int64_t>(1, (waves + kCUs - 1) / kCUs));
   if (tu.wo_gemv_waves > 0) W = std::min(tu.wo_gemv_waves, kGvMaxWaves);
   const int64_t threads = 64LL * W;
-  if (M * (K / 8) > kGvXPieces * threads) return pl;  // activation pieces per thread
-  const size_t lds = (size_t)(M <= 1 ? 1 : 2) * ((size_t)K * 2 + (size_t)ppr * 4);
+  if (K / 8 > kGvXPR * threads) return pl;  // activation pieces per thread and row
+  const size_t lds = (size_t)gemv_rows(M) * ((size_t)K * 2 + (size_t)ppr * 4);
   if (lds > (size_t)kGvLds) return pl;
   pl.RW = RW;
   pl.W = W;
