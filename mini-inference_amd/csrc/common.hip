@@ -42,6 +42,10 @@ Tuning read_tuning() {
   t.wo_prefill_min_m = pmm && atoi(pmm) > 0 ? atoi(pmm) : 65;
   const char* pps = getenv("MIQ_WO_PREFILL_S");
   t.wo_prefill_s = pps ? atoi(pps) : 0;
+  const char* wmt = getenv("MIQ_WO_WIDE_MT");
+  t.wo_wide_mt = wmt ? atoi(wmt) : -1;
+  const char* wmm = getenv("MIQ_WO_WIDE_MIN_M");
+  t.wo_wide_min_m = wmm && atoi(wmm) > 0 ? atoi(wmm) : 65;
   t.fp8_old = flag("MIQ_FP8_OLD");
   const char* fw = getenv("MIQ_FP8_WAVES");
   t.fp8_four_waves = fw && atoi(fw) == 4;

@@ -588,7 +588,7 @@ paged_decode_split8_kernel(AttnParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const __amdgpu_buffer_rsrc_t rs = page_rsrc(p.v, cpg[2 * s + (i >> 1)]);
-          const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, ((8 * i) & 15 | (lane >> 3)) * (int)p.kvs_t + dseg, 0,
+          const auto v = __builtin_amdgcn_raw_buffer_load_b128(rs, (((8 * i) & 15) | (lane >> 3)) * (int)p.kvs_t + dseg, 0,
                                                                2 /* nt */);
           vr[bi][s][i] = *reinterpret_cast<const uint4*>(&v);
         }

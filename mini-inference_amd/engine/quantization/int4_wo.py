@@ -39,10 +39,10 @@ class Int4WeightOnly(QuantMethod):
     def linear(self, x, qweight, scale, zero=None):
         """base.py:20-24 with the int4 dequantize.
 
-        Up to kernels.quant_ops.PREFILL_MAX_M[4] rows the fused GEMM runs (unpack and scale
-        inside the K loop: the decode kernels up to 64 rows, the prefill kernel above);
-        larger inputs dequantize with the kernel and use the device GEMM, which is faster
-        there."""
+        The fused GEMM runs for every M (the decode kernels up to 64 rows, the prefill and
+        wide kernels above: the weights are unpacked inside the K loop and never written out
+        as bf16); shapes outside its contract (see ops.w4a16_supported) dequantize with the
+        HIP kernel and use the device GEMM."""
         if ops.w4a16_supported(x, qweight, scale):
             return ops.w4a16_linear(x, qweight, scale, zero)
         w = self.dequantize(qweight, scale, zero).to(x.dtype)

@@ -24,9 +24,9 @@ class Int8WeightOnly(QuantMethod):
     def linear(self, x, qweight, scale):
         """int8_wo.py:17-21: (x @ q^T) * scale.
 
-        Up to kernels.quant_ops.PREFILL_MAX_M[8] rows the fused GEMM runs (the int8 codes
-        are read once, no bf16 weight is written); larger inputs use the reference's own
-        formula with the device GEMM, which is faster there."""
+        The fused GEMM runs for every M (the int8 codes are read once, no bf16 weight is
+        written); shapes outside its contract (see ops.w8a16_supported) use the reference's
+        own formula with the device GEMM."""
         if ops.w8a16_supported(x, qweight):
             return ops.w8a16_linear(x, qweight, scale)
         y = torch.nn.functional.linear(x, qweight.to(x.dtype))

@@ -10,11 +10,10 @@ import torch
 
 from kernels import _lib as L
 
-SKINNY_MAX_M = 64  # decode kernels up to 64 activation rows; above, the prefill kernel
-# Largest M for which the fused prefill kernel is used by the quantization methods; above it
-# the methods dequantize and call the device GEMM, which measured faster on MI355X from
-# about these sizes (INT4: M = 1536 at 19456 x 2560; INT8: M = 1024 at 2560 x 9728).
-PREFILL_MAX_M = {4: 1024, 8: 768}
+SKINNY_MAX_M = 64  # decode kernels up to 64 activation rows; above, the prefill kernels
+# The fused weight-only GEMMs take any M whose activations stay below 2^31 elements (their
+# buffer descriptors address 32-bit offsets).
+MAX_X_ELEMS = 1 << 31
 
 
 def _rows(t):
@@ -73,7 +72,7 @@ def w8a16_linear(x, qweight, scale):
 
 def w8a16_supported(x, qweight):
     M = _rows(x)
-    return (x.dtype == torch.bfloat16 and 1 <= M <= PREFILL_MAX_M[8] and x.shape[-1] % 128 == 0
+    return (x.dtype == torch.bfloat16 and M >= 1 and M * x.shape[-1] < MAX_X_ELEMS and x.shape[-1] % 128 == 0
             and qweight.shape[-2] % 16 == 0 and qweight.dim() == 2)
 
 
@@ -133,7 +132,7 @@ def w4a16_supported(x, qweight, scale):
     if scale.shape[-1] == 0 or K % scale.shape[-1]:
         return False
     group = K // scale.shape[-1]
-    return (x.dtype == torch.bfloat16 and 1 <= M <= PREFILL_MAX_M[4] and group % 128 == 0
+    return (x.dtype == torch.bfloat16 and M >= 1 and M * K < MAX_X_ELEMS and group % 128 == 0
             and qweight.shape[-2] % 16 == 0 and qweight.dim() == 2)
 
 

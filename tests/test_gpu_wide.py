@@ -1,0 +1,141 @@
+"""The wide weight-only GEMM (long prefill chunks) vs the CPU oracle.
+
+The wide kernel dequantizes each weight once per workgroup into bf16 and multiplies on the
+bf16 MFMA, as the reference's own path does (int4_wo.py:33-42 / int8_wo.py:14-21, then
+base.py:20-24). Its int4 weights are q * s + z rounded once to bf16, where the reference
+rounds q * s and then the sum: about half of the asymmetric weights differ by an ulp, and
+the reference's weights are the further from the exact ones. So, as for the other weight-
+only kernels, it is held to |got - want| <= 1e-2 + 2e-2 |want| elementwise against the
+fp32-accumulated product on the exactly dequantized weights, and to the reference test's
+norm-wise bound (rel < 0.01, tests/test_quantizaton.py:60-72) against the reference's own
+bf16 formula. INT8 codes are exact in bf16.
+
+Every shape runs with each tile height forced (MIQ_WO_WIDE_MT = 1, 2, 3), with the planned
+choice, and with the wide kernel off (the prefill kernel), and the shared workspace must be
+all zeros afterwards (the packed activations are cleared again).
+"""
+import pytest
+import torch
+
+from oracle import quant as O
+from test_gpu_gemm import DEV, case, make_w, make_x, rel, within, workspace_is_zero
+
+pytestmark = pytest.mark.gpu
+
+# (M, N, K, group): ragged M (not a multiple of any tile height), N with a partial
+# 128-row weight block (2576 = 20 * 128 + 16), one and three k-steps, groups of 1 to 4 steps
+WIDE_SHAPES = [(1300, 2560, 512, 128), (520, 2576, 1536, 256), (777, 1024, 128, 128), (300, 4096, 384, 128),
+               (2048, 2560, 2560, 512)]
+TILES = {"mt1": "1", "mt2": "2", "mt3": "3", "planned": None, "off": "0"}
+
+
+_CACHE = {}
+
+
+def int4_case(M, N, K, group, symmetric, sdt):
+    """Inputs and both oracles of a shape, computed once for all tile settings."""
+    key = ("int4", M, N, K, group, symmetric, sdt)
+    if key not in _CACHE:
+        w = make_w(N, K, 90)
+        x = make_x(M, K, 91)
+        q = O.int4_quantize_symmetric(w, group, sdt) if symmetric else O.int4_quantize(w, group, sdt)
+        _CACHE.clear()
+        _CACHE[key] = (x, q, O.int4_linear_fp32(x, **q), O.int4_linear(x, **q))
+    return _CACHE[key]
+
+
+def int8_case(M, N, K, sdt):
+    key = ("int8", M, N, K, sdt)
+    if key not in _CACHE:
+        w = make_w(N, K, 92)
+        x = make_x(M, K, 93)
+        q = O.int8_quantize(w, sdt)
+        _CACHE.clear()
+        _CACHE[key] = (x, q, O.int8_linear_fp32(x, **q), O.int8_linear(x, **q))
+    return _CACHE[key]
+
+
+@pytest.mark.parametrize("M,N,K,group", WIDE_SHAPES)
+@pytest.mark.parametrize("symmetric,sdt", [(False, torch.bfloat16), (True, torch.bfloat16), (False, torch.float16),
+                                           (False, torch.float32)])
+@pytest.mark.parametrize("tiles", list(TILES))
+def test_w4a16_wide(M, N, K, group, symmetric, sdt, tiles, miq_env):
+    from kernels import quant_ops as ops
+    case(f"w4a16 wide M={M} N={N} K={K} g={group} sym={symmetric} {sdt} tiles={tiles}")
+    if TILES[tiles] is not None:
+        miq_env("MIQ_WO_WIDE_MT", TILES[tiles])
+    x, q, want, ref = int4_case(M, N, K, group, symmetric, sdt)
+    y = ops.w4a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV),
+                         None if symmetric else q["zero"].to(DEV))
+    assert y.shape == (M, N)
+    within(y, want)
+    assert rel(y, ref) < 0.01
+    assert workspace_is_zero()
+
+
+@pytest.mark.parametrize("M,N,K", [(1300, 2560, 512), (520, 2576, 1536), (777, 1024, 128), (2048, 2560, 2560)])
+@pytest.mark.parametrize("sdt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("tiles", list(TILES))
+def test_w8a16_wide(M, N, K, sdt, tiles, miq_env):
+    from kernels import quant_ops as ops
+    case(f"w8a16 wide M={M} N={N} K={K} {sdt} tiles={tiles}")
+    if TILES[tiles] is not None:
+        miq_env("MIQ_WO_WIDE_MT", TILES[tiles])
+    x, q, want, ref = int8_case(M, N, K, sdt)
+    y = ops.w8a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV))
+    within(y, want)
+    assert rel(y, ref) < 0.01
+    assert workspace_is_zero()
+
+
+def test_wide_strided_rows_and_output():
+    """Activation rows with a row stride above K and an output written into a wider buffer
+    (row stride above N, so the 8-byte output stores fall back to 2-byte ones)."""
+    from kernels import _lib as L
+    from kernels import quant_ops as ops
+    M, N, K = 1100, 2560, 1024
+    case(f"wide strided M={M} N={N} K={K}")
+    w = make_w(N, K, 94)
+    xbig = make_x(M, K + 64, 95)
+    x = xbig[:, :K]
+    q = O.int4_quantize(w, 128)
+    want = O.int4_linear_fp32(x, **q)
+    xd = xbig.to(DEV)[:, :K]
+    qd, sd, zd = (q[k].to(DEV) for k in ("qweight", "scale", "zero"))
+    buf = torch.full((M, N + 6), 7.0, dtype=torch.bfloat16, device=DEV)
+    nbytes = L.load().miq_wo_gemm_workspace_bytes(M, N, K, 4)
+    ws = L.wo_workspace(xd.device, nbytes)
+    L.call("miq_w4a16_gemm", L.ptr(xd), xd.stride(0), L.ptr(qd), L.ptr(sd), L.ptr(zd), L.dtype_code(sd.dtype), 128,
+           L.ptr(buf), buf.stride(0), M, N, K, L.ptr(ws), ws.numel(), L.stream(xd.device))
+    within(buf[:, :N], want)
+    assert bool((buf[:, N:].float() == 7.0).all())
+    assert workspace_is_zero()
+    torch.testing.assert_close(buf[:, :N], ops.w4a16_linear(xd, qd, sd, zd), rtol=0, atol=0)
+
+
+def test_wide_graph_replays_match_eager():
+    """Pack, multiply and clear under HIP graph capture: every replay (with eager work and a
+    synchronization between replays) matches the eager result bit for bit."""
+    from kernels import quant_ops as ops
+    M, N, K = 1024, 2560, 1024
+    w = make_w(N, K, 96)
+    q = O.int4_quantize(w, 128)
+    qd, sd, zd = (q[k].to(DEV) for k in ("qweight", "scale", "zero"))
+    x = make_x(M, K, 97).to(DEV)
+    eager = ops.w4a16_linear(x, qd, sd, zd)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.w4a16_linear(x, qd, sd, zd)  # workspace for this stream exists before capture
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            y = ops.w4a16_linear(x, qd, sd, zd)
+    torch.cuda.current_stream().wait_stream(s)
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        torch.testing.assert_close(y, eager, rtol=0, atol=0)
+        _ = (x * 2).sum().item()  # eager work between replays
+    with torch.cuda.stream(s):
+        assert workspace_is_zero()
