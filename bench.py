@@ -46,6 +46,7 @@ import torch  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
 FP8_PEAK_TFLOPS = 5000.0     # MI355X dense FP8 MFMA, published
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, published
 ROTATE_BYTES = 600 * 2 ** 20  # > 2 x MALL
 METRIC = "quantized decode GEMM GB/s (% HBM peak) at M=1..64; FP8-KV attn µs/step"
 MS = (1, 8, 32, 64)
@@ -234,6 +235,41 @@ def bench_int4_asym(dev):
     res = per_m(cfg, int4_launch, int4_bytes, dev)
     del cfg
     return res
+
+
+def bench_wo_prefill(dev):
+    """Weight-only GEMMs on prefill-sized M (libmiq's planner picks the wide kernel where its
+    128 x 128 MT tiles fill the GPU, the prefill kernel below that), against the
+    library route the reference itself takes for every M (dequantize to bf16, then
+    F.linear on hipBLASLt: int4_wo.py:33-42 + base.py:20-24, int8_wo.py:17-21)."""
+    import torch.nn.functional as F
+    from kernels import quant_ops as ops
+    out = {}
+    reps = 10
+    for name, N, K in (("int4_down_proj_2560x9728", 2560, 9728), ("int8_gate_up_19456x2560", 19456, 2560)):
+        w = (torch.randn(N, K, generator=gen(11)) * 0.02).to(torch.bfloat16).to(dev)
+        if name.startswith("int4"):
+            q, s, z = ops.int4_quantize(w, 128, torch.bfloat16, symmetric=True)
+            fused = lambda x: ops.w4a16_linear(x, q, s, z)  # noqa: E731
+            lib = lambda x: F.linear(x, ops.int4_dequantize(q, s, z))  # noqa: E731
+        else:
+            q, s = ops.int8_quantize(w, torch.float32)
+            fused = lambda x: ops.w8a16_linear(x, q, s)  # noqa: E731
+            lib = lambda x: F.linear(x, q.to(torch.bfloat16)) * s.reshape(-1).to(torch.bfloat16)  # noqa: E731
+        del w
+        rows = {}
+        for M in (256, 1024, 2048):
+            x = torch.randn(M, K, generator=gen(12)).to(torch.bfloat16).to(dev)
+            t = min(time_graph([lambda: fused(x)] * reps) / reps for _ in range(2))
+            t_lib = min(time_graph([lambda: lib(x)] * reps) / reps for _ in range(2))
+            tf = 2.0 * M * N * K / t / 1e12
+            rows[str(M)] = {"us": round(t * 1e6, 1), "TFLOP/s": round(tf, 1),
+                            "pct_bf16_peak": round(100 * tf / BF16_PEAK_TFLOPS, 1),
+                            "dequant_plus_hipblaslt_us": round(t_lib * 1e6, 1)}
+        out[name] = rows
+        del q, s
+        torch.cuda.empty_cache()
+    return out
 
 
 def bench_fp8(dev):
@@ -676,6 +712,7 @@ SECTIONS = {
     "int4_w4a16_zero_point_per_M": bench_int4_asym,
     "int8_w8a16_gate_up_per_M": bench_int8,
     "fp8_prefill_gemm": bench_fp8,
+    "wo_prefill_large_M": bench_wo_prefill,
     "paged_decode_fp8_kv": lambda dev: bench_attention(dev, "fp8"),
     "paged_decode_int8_kv": lambda dev: bench_attention(dev, "int8"),
     "moe_int4_layer": bench_moe,
