@@ -116,12 +116,15 @@ int miq_fp8_dequantize(const uint8_t* q, const float* scale, int64_t rows, int64
 
 /* ------------------------------------------------------------------ weight-only GEMMs
  * Any M >= 1: decode kernels up to M = 64, a dequantize-in-the-K-loop MFMA GEMM above
- * (prefill), which splits K when the output has fewer 64 x 128 tiles than CUs.
- * Workspace for the split-K reduction of the two weight-only GEMMs. Its first 16384
- * bytes hold arrival counters that must be zero before the first call (zero the whole
- * buffer once when allocating it); every call leaves them at zero again, and the fp32
- * partials that follow never overlap them. Calls that share one
- * workspace must be ordered (same stream). */
+ * (prefill), which splits K when the output has fewer 64 x 128 tiles than CUs, and, where
+ * its 128 x 128..384 tiles fill the GPU (long prefill chunks), a GEMM that dequantizes
+ * each weight block once per workgroup for the bf16 MFMA.
+ * Workspace for the split-K reduction of the two weight-only GEMMs and for the last
+ * kernel's packed activations. Its first 16384 bytes hold arrival counters that must be
+ * zero before the first call (zero the whole buffer once when allocating it); every call
+ * leaves the whole workspace at zero again (counters, fp32 partials and packed
+ * activations alike). A workspace below this size for a long prefill call makes it take
+ * the prefill kernel. Calls that share one workspace must be ordered (same stream). */
 size_t miq_wo_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits);
 
 /* Replaces Int8WeightOnly.linear (int8_wo.py:17-21):
@@ -135,7 +138,9 @@ int miq_w8a16_gemm(const void* x, int64_t ldx, const int8_t* q, const void* scal
 /* Replaces Int4WeightOnly.linear = QuantMethod.linear over Int4WeightOnly.dequantize
  * (engine/quantization/base.py:20-24, int4_wo.py:33-42): y = bf16(x @ W^T) with
  * W = q * scale + zero (zero == NULL: W = (q - 8) * scale), evaluated in fp32 as
- * scale * (x . q) + zero * sum(x) per group. x: bf16 [M, K]; q: uint8 [N, K/2];
+ * scale * (x . q) + zero * sum(x) per group (the wide kernel of long prefill calls
+ * multiplies W rounded once to bf16, as the reference's bf16 weights are). x: bf16 [M, K];
+ * q: uint8 [N, K/2];
  * scale/zero: [N, K/group] of sz_dtype (bf16/f16/f32). M >= 1, group % 128 == 0,
  * K % group == 0, N % 16 == 0. */
 int miq_w4a16_gemm(const void* x, int64_t ldx, const uint8_t* q, const void* scale,
@@ -146,8 +151,9 @@ int miq_w4a16_gemm(const void* x, int64_t ldx, const uint8_t* q, const void* sca
 /* miq_w4a16_gemm without a workspace argument, for callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc). No counterpart in the reference. The split-K scratch is a static device array
- * of 32 MiB that each GPU holds until the process ends; shapes whose
- * miq_wo_gemm_workspace_bytes(M, N, K, 4) exceeds it are rejected (MIQ_ERR_INVALID). Every call on a GPU shares that GPU's array: calls that
+ * of 32 MiB that each GPU holds until the process ends; shapes whose split-K scratch
+ * exceeds it are rejected (MIQ_ERR_INVALID); long prefill calls whose packed activations
+ * would not fit take the prefill kernel. Every call on a GPU shares that GPU's array: calls that
  * overlap on one GPU (two streams, two threads) race and give wrong results; calls ordered
  * on one stream are safe. Allocates nothing; the first call on a device looks up the
  * array's address there. Same arguments and results as miq_w4a16_gemm. */

@@ -21,7 +21,8 @@ int wo_panel_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ld
                     int N, int K, void* workspace, size_t ws_bytes, size_t counter_bytes, hipStream_t st,
                     const char* name, bool& launched);
 constexpr size_t kWoCounterBytes = 16384;  // the workspace's counter area (4096 ints)
-size_t wo_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits, size_t counter_bytes);
+size_t wo_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits, size_t counter_bytes,
+                                  bool with_wide);
 int wo_prefill_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw, const void* scale,
                       const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int64_t M,
                       int N, int K, void* workspace, size_t ws_bytes, size_t counter_bytes, hipStream_t st,
@@ -92,13 +93,21 @@ int run(int kind, const WoArgs& p, void* workspace, size_t ws_bytes, hipStream_t
 
 using namespace miq;
 
-extern "C" size_t miq_wo_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits) {
+namespace miq {
+// Workspace bytes of a weight-only GEMM call; with_wide = false leaves out the wide kernel's
+// packed activations (a call given less than that takes the prefill kernel instead).
+size_t wo_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits, bool with_wide) {
   const size_t prefill = M >= tuning().wo_prefill_min_m && N >= 1 && K >= kStepK
-                             ? wo_prefill_workspace_bytes(M, N, K, weight_bits, kWoCounterBytes) : 0;
+                             ? wo_prefill_workspace_bytes(M, N, K, weight_bits, kWoCounterBytes, with_wide) : 0;
   const size_t stream = wo_stream_workspace_bytes(M, N, K, weight_bits);
   if (weight_bits != 4 || M < 1 || N < 1 || K < kStepK) return std::max({kWoCounterBytes, stream, prefill});
   return std::max({kWoCounterBytes, stream, prefill, kWoCounterBytes + wo_panel_partial_bytes(M, N, K),
                    kWoCounterBytes + wo_tile_pair_bytes(M, N)});
+}
+}  // namespace miq
+
+extern "C" size_t miq_wo_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits) {
+  return wo_gemm_workspace_bytes(M, N, K, weight_bits, true);
 }
 
 extern "C" int miq_w8a16_gemm(const void* x, int64_t ldx, const int8_t* q, const void* scale,
@@ -189,7 +198,8 @@ int scratch_of_current_device(void** out) {
 extern "C" int miq_w4a16_gemm_noalloc(const void* x, int64_t ldx, const uint8_t* q, const void* scale,
                                       const void* zero, int sz_dtype, int64_t group, void* y, int64_t ldy,
                                       int64_t M, int64_t N, int64_t K, void* stream) {
-  const size_t need = miq_wo_gemm_workspace_bytes(M, N, K, 4);
+  // the wide kernel runs here only where its packed activations fit the scratch as well
+  const size_t need = wo_gemm_workspace_bytes(M, N, K, 4, false);
   MIQ_REQUIRE(need <= kScratchBytes,
               "w4a16_gemm_noalloc: M=%lld N=%lld K=%lld needs %zu bytes of split-K scratch, above the %zu bytes "
               "the library holds per GPU; use miq_w4a16_gemm with a workspace",

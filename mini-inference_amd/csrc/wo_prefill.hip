@@ -503,12 +503,14 @@ static int wide_mt(int64_t M, int64_t N, int64_t K, int64_t ldw) {
   return mt > 0 && wo_wide_fits(M, K, N, ldw, mt) ? mt : 0;
 }
 
-// Workspace bytes of a prefill call: the counter area, then the split-K partials.
-size_t wo_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits, size_t counter_bytes) {
+// Workspace bytes of a prefill call: the counter area, then the split-K partials or (with_wide)
+// the wide kernel's packed activations, whichever is larger.
+size_t wo_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits, size_t counter_bytes,
+                                  bool with_wide) {
   const PrefillPlan pl = plan_prefill(weight_bits == 4 ? KIND_INT4 : KIND_INT8, M, N, K, counter_bytes);
   const size_t split = pl.S > 1 ? counter_bytes + pl.partial_bytes : 0;
   // the wide kernel's packed activations (ldw is not known here: its limit is checked at launch)
-  const int wmt = wide_mt(M, N, K, 0);
+  const int wmt = with_wide ? wide_mt(M, N, K, 0) : 0;
   const size_t wide = wmt > 0 ? counter_bytes + wo_wide_pack_bytes(M, K, wmt) : 0;
   return std::max(split, wide);
 }

@@ -6,13 +6,13 @@
 // wavefront w owns activation rows 32 MT w .. 32 MT w + 32 MT - 1 against all 128 weight
 // rows (4 MT accumulator tiles of 32 x 32 in AGPRs). Per 128-k step the workgroup
 // dequantizes its 128 x 128 weight block once, into LDS, as bf16 MFMA operand fragments:
-//   int4: w = fma(q, s, z) with the group's scale and zero (symmetric codes: z = -8 s), one
-//         fp32 fma and one round-to-nearest-even conversion per element (q * s is exact in
-//         fp32, so this is q * s + z rounded once);
+//   int4: the reference's weight, bit for bit: bf16(SD(SD(q s) + z)) in the scale dtype SD's
+//         arithmetic (symmetric codes: bf16(SD((q - 8) s))), 3 to 5 VALU instructions per
+//         code;
 //   int8: w = q, exact in bf16; the per-row scale is applied to the output as int8_wo does,
 //         y = bf16(bf16(acc) * bf16(s)).
-// The dequantize work (about 23 VALU instructions per 8 int4 codes, 8 codes per thread and
-// sub-step) is done once per workgroup and feeds 4 MT MFMAs per fragment per wavefront
+// The dequantize work (about 23 (symmetric) to 43 (zero points) VALU instructions per 8
+// int4 codes, 8 codes per thread and sub-step) is done once per workgroup and feeds 4 MT MFMAs per fragment per wavefront
 // (the decode-shaped prefill kernel instead unpacks the weights in every wavefront and
 // corrects the +128 code offset with per-group activation sums: about 7 VALU instructions
 // per MFMA, which bounds it well below the MFMA peak at large M).
@@ -100,20 +100,57 @@ __device__ inline uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// 8 int4 codes of one word (low nibble first) -> 8 bf16 fma(q, s, z), natural k order.
+// The two bf16 values of a packed pair, widened to fp32 (exact).
+__device__ inline float bf16_lo(uint32_t p) { return __builtin_bit_cast(float, p << 16); }
+__device__ inline float bf16_hi(uint32_t p) { return __builtin_bit_cast(float, p & 0xffff0000u); }
+
+// The reference's dequantized int4 weight (int4_wo.py:33-42 and its symmetric form), for
+// codes q (as fp32), computed in the scale dtype's arithmetic (each op rounded to it, as
+// torch does on the CPU) and then rounded to bf16 for the matmul, as
+// QuantMethod.linear's .to(x.dtype) does (base.py:20-24), so the weights are the
+// reference's bit for bit:
+//   zero points:  w = bf16(SD(SD(q s) + z));   symmetric: w = bf16(SD((q - 8) s)),
+// with z = -8 s passed for the symmetric form. q s is exact in fp32 for bf16 / f16 scales.
+template <int SD, bool HZ>
+__device__ inline uint32_t dequant_pair(float q0, float q1, float s, float z) {
+  if constexpr (!HZ) {
+    // (q - 8) s = fma(q, s, -8 s), rounded once to fp32 (exact for bf16 / f16 scales)
+    float a = __builtin_fmaf(q0, s, z), b = __builtin_fmaf(q1, s, z);
+    if constexpr (SD == MIQ_F16) {
+      a = static_cast<float>(static_cast<_Float16>(a));
+      b = static_cast<float>(static_cast<_Float16>(b));
+    }
+    return pack_bf16x2(a, b);
+  } else if constexpr (SD == MIQ_BF16) {
+    const uint32_t p = pack_bf16x2(q0 * s, q1 * s);  // bf16(q s), q s exact in fp32
+    return pack_bf16x2(bf16_lo(p) + z, bf16_hi(p) + z);
+  } else if constexpr (SD == MIQ_F16) {
+    const float a = static_cast<float>(static_cast<_Float16>(q0 * s));
+    const float b = static_cast<float>(static_cast<_Float16>(q1 * s));
+    return pack_bf16x2(static_cast<float>(static_cast<_Float16>(a + z)),
+                       static_cast<float>(static_cast<_Float16>(b + z)));
+  } else {
+    // fp32: the product and the sum each rounded; the empty asm statement keeps the
+    // compiler from contracting them into one fma
+    float a = q0 * s, b = q1 * s;
+    asm("" : "+v"(a), "+v"(b));
+    return pack_bf16x2(a + z, b + z);
+  }
+}
+
+// 8 int4 codes of one word (low nibble first) -> the 8 reference weights, natural k order.
 // The masked words pass through an empty asm statement so that the byte converts stay
 // v_cvt_f32_ubyte{0..3} on the masked words (otherwise each nibble becomes its own
 // bitfield extract).
+template <int SD, bool HZ>
 __device__ inline uint4 dequant_u4(uint32_t w, float s, float z) {
   uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
   asm volatile("" : "+v"(lo), "+v"(hi));
   uint4 o;
-  o.x = pack_bf16x2(__builtin_fmaf(static_cast<float>(lo & 0xffu), s, z), __builtin_fmaf(static_cast<float>(hi & 0xffu), s, z));
-  o.y = pack_bf16x2(__builtin_fmaf(static_cast<float>((lo >> 8) & 0xffu), s, z),
-                    __builtin_fmaf(static_cast<float>((hi >> 8) & 0xffu), s, z));
-  o.z = pack_bf16x2(__builtin_fmaf(static_cast<float>((lo >> 16) & 0xffu), s, z),
-                    __builtin_fmaf(static_cast<float>((hi >> 16) & 0xffu), s, z));
-  o.w = pack_bf16x2(__builtin_fmaf(static_cast<float>(lo >> 24), s, z), __builtin_fmaf(static_cast<float>(hi >> 24), s, z));
+  o.x = dequant_pair<SD, HZ>(static_cast<float>(lo & 0xffu), static_cast<float>(hi & 0xffu), s, z);
+  o.y = dequant_pair<SD, HZ>(static_cast<float>((lo >> 8) & 0xffu), static_cast<float>((hi >> 8) & 0xffu), s, z);
+  o.z = dequant_pair<SD, HZ>(static_cast<float>((lo >> 16) & 0xffu), static_cast<float>((hi >> 16) & 0xffu), s, z);
+  o.w = dequant_pair<SD, HZ>(static_cast<float>(lo >> 24), static_cast<float>(hi >> 24), s, z);
   return o;
 }
 
@@ -194,7 +231,7 @@ wo_wide_kernel(WideParams p) {
     if constexpr (I4) {
       const uint4& wv4 = wreg[set][q >> 2];
       const uint32_t d = (q & 3) == 0 ? wv4.x : (q & 3) == 1 ? wv4.y : (q & 3) == 2 ? wv4.z : wv4.w;
-      return dequant_u4(d, sc, zz);
+      return dequant_u4<SD, HZ>(d, sc, zz);
     } else {
       const uint4& wv4 = wreg[set][q >> 1];
       return (q & 1) ? dequant_i8(wv4.z, wv4.w) : dequant_i8(wv4.x, wv4.y);

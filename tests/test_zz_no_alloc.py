@@ -8,6 +8,7 @@ import pytest
 import torch
 
 from oracle import quant as O
+from test_gpu_wide import int4_ref_weights_product, wide_planned
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -47,8 +48,11 @@ def test_noalloc_matches_workspace_entry_point():
     # prefill kernel with a K split (200 rows: 80 tiles), a smaller panel launch, two
     # tile-kernel launches of the two-half plan (exchange words in the scratch), then the
     # first shape again
-    shapes = [(64, 2560, 9728, 128, True), (200, 2560, 9728, 128, False), (40, 1280, 4096, 256, False),
-              (16, 2560, 9728, 128, True), (8, 512, 1024, 128, False), (64, 2560, 9728, 128, True)]
+    # the wide kernel (1024 rows: its packed activations, 2 MiB, go in the scratch and are
+    # cleared again) comes between the prefill and panel launches
+    shapes = [(64, 2560, 9728, 128, True), (200, 2560, 9728, 128, False), (1024, 2560, 1024, 128, False),
+              (40, 1280, 4096, 256, False), (16, 2560, 9728, 128, True), (8, 512, 1024, 128, False),
+              (64, 2560, 9728, 128, True)]
     for i, (M, N, K, group, sym) in enumerate(shapes):
         case(f"noalloc call {i}: M={M} N={N} K={K} g={group} sym={sym}")
         x, q = operands(M, N, K, group, sym, seed=70 + (i % 3))
@@ -57,10 +61,34 @@ def test_noalloc_matches_workspace_entry_point():
         want = with_workspace(x, q)
         torch.cuda.synchronize()
         assert torch.equal(y, want), (y.float() - want.float()).abs().max().item()
-        # and within the north-star tolerance of the fp32 oracle
-        ref = O.int4_linear_fp32(x.cpu(), **{k: v.cpu() for k, v in q.items()})
+        # and within the north-star tolerance of the fp32 oracle: the exactly dequantized
+        # weights, or for the wide kernel the reference's own bf16 weights (test_gpu_wide)
+        qc = {k: v.cpu() for k, v in q.items()}
+        ref = (int4_ref_weights_product(x.cpu(), qc) if M > 64 and wide_planned(M, N)
+               else O.int4_linear_fp32(x.cpu(), **qc))
         err = (y.float().cpu() - ref).abs()
         assert (err <= 1e-2 + 2e-2 * ref.abs()).all()
+
+
+def test_noalloc_large_prefill_takes_the_prefill_kernel():
+    """2048 x 9728 activations: the wide kernel's packed copy (40 MiB) would not fit the
+    32 MiB scratch, so the entry point runs the prefill kernel (split-K partials within the
+    scratch) where the workspace entry point runs the wide kernel: both within the
+    north-star tolerance of the fp32 oracle, and the scratch left clean for the next call."""
+    M, N, K, group = 2048, 2560, 9728, 128
+    case(f"noalloc M={M} N={N} K={K}: prefill kernel in place of the wide one")
+    x, q = operands(M, N, K, group, False, seed=75)
+    rc, y = noalloc(x, q, group)
+    assert rc == 0
+    qc = {k: v.cpu() for k, v in q.items()}
+    exact = O.int4_linear_fp32(x.cpu(), **qc)  # the prefill kernel multiplies exact weights
+    ref_w = int4_ref_weights_product(x.cpu(), qc)  # the wide kernel: the reference's bf16 weights
+    for got, want in ((y, exact), (with_workspace(x, q), ref_w)):
+        err = (got.float().cpu() - want).abs()
+        assert (err <= 1e-2 + 2e-2 * want.abs()).all()
+    x, q = operands(16, 2560, 9728, 128, True, seed=76)
+    rc, y = noalloc(x, q, 128)
+    assert rc == 0 and torch.equal(y, with_workspace(x, q))
 
 
 def test_noalloc_rejects_shapes_beyond_the_scratch():
