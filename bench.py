@@ -633,19 +633,70 @@ def cpu_moe(budget=6.0):
 
 
 # ---------------------------------------------------------------- HBM traffic (counters)
+# The phases of the counter child after the headline, in order: (breakdown entry, key)
+TRAFFIC_PHASES = [("int8_w8a16_gate_up_per_M", "M=1"), ("int8_w8a16_gate_up_per_M", "M=64"),
+                  ("fp8_prefill_gemm", None), ("paged_decode_fp8_kv", None), ("moe_int4_layer", None)]
+TRAFFIC_CALLS = 2  # calls per phase
+
+
 def traffic_child():
-    """The run the counter passes watch: four headline launches per round, eagerly, then
+    """The run the counter passes watch: four headline launches per round, eagerly; then
+    TRAFFIC_CALLS calls of each TRAFFIC_PHASES configuration (INT8 gate_up at M = 1 and 64,
+    the FP8 GEMM, FP8-KV paged decode at the default partition, the INT4 MoE layer); then
     the two calibration kernels (a 256 MiB fill, and a sum over a 256 MiB buffer that a
-    second fill has evicted from the MALL)."""
+    second fill has evicted from the MALL). A tiny miq_stream_read launch ends each phase,
+    so the parent can split the dispatches."""
     from kernels import _lib
-    _lib.load()
+    from kernels import quant_ops as ops
+    lib = _lib.load()
     dev = torch.device("cuda:0")
+    mark_buf = torch.zeros(4096, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+
+    def marker():
+        torch.cuda.synchronize()
+        lib.miq_stream_read(mark_buf.data_ptr(), 4096, sink.data_ptr(), torch.cuda.current_stream(dev).cuda_stream)
+        torch.cuda.synchronize()
+
     cfg = int4_setup(dev)
     for i in range(3):
         for j, M in enumerate(MS):
             int4_launch(cfg, M, 4 * i + j)()
-    torch.cuda.synchronize()
     del cfg
+    marker()
+    c8 = int8_setup(dev)
+    for M in (1, 64):
+        for i in range(TRAFFIC_CALLS):
+            q, sc = c8["copies"][i % len(c8["copies"])]
+            ops.w8a16_linear(c8["x"][M], q, sc)
+        marker()
+    del c8
+    M, N, K = 2048, 6144, 2560
+    w = (torch.randn(N, K, generator=gen(5)) * 0.02).to(torch.bfloat16).to(dev)
+    wq, ws = ops.fp8_quantize_rows(w)
+    xq, xs = ops.fp8_quantize_rows(torch.randn(M, K, generator=gen(6)).to(torch.bfloat16).to(dev))
+    torch.cuda.synchronize()
+    marker()
+    for _ in range(TRAFFIC_CALLS):
+        ops.fp8_gemm(xq, xs, wq, ws)
+    marker()
+    del w, wq, ws, xq, xs
+    from kernels.paged_attention import paged_decode_attention
+    a = attention_inputs(dev, "fp8")
+    for i in range(TRAFFIC_CALLS):
+        kc, vc, ks, vs = a["caches"][i % len(a["caches"])]
+        paged_decode_attention(a["q"], kc, vc, a["table"], a["lens"], a["page"], 128 ** -0.5, a["max_len"],
+                               k_scale=ks, v_scale=vs)
+    marker()
+    del a
+    from kernels.fused_moe import fused_moe_int4
+    c = moe_setup(dev, copies=TRAFFIC_CALLS)
+    for i in range(TRAFFIC_CALLS):
+        (gq, gs), (dq, ds) = c["sets"][i]
+        fused_moe_int4(c["hidden"], c["idx"], c["w"], gq, gs, None, dq, ds, None)
+    marker()
+    del c
+    torch.cuda.synchronize()
     torch.cuda.empty_cache()
     a = torch.empty(PROBE_BYTES // 4, dtype=torch.float32, device=dev).fill_(1.0)
     b = torch.empty_like(a).fill_(2.0)
@@ -669,8 +720,9 @@ def _pmc_pass(counter, outdir):
 
 
 def measure_traffic():
-    """Per-launch HBM bytes of the headline kernels from FETCH_SIZE and WRITE_SIZE passes.
-    Returns (dict, None) or (None, reason)."""
+    """Per-launch HBM bytes from FETCH_SIZE and WRITE_SIZE passes: the headline kernels per
+    M, and per call every TRAFFIC_PHASES configuration. Returns (dict, None) or
+    (None, reason)."""
     if shutil.which("rocprofv3") is None:
         return None, "rocprofv3 not found"
     tmp = tempfile.mkdtemp(prefix="miq_traffic_", dir="/tmp")
@@ -682,28 +734,83 @@ def measure_traffic():
     finally:
         shutil.rmtree(tmp, ignore_errors=True)
 
-    def ours(rows):
-        return [r for r in rows if "wo_" in r["Kernel_Name"] and "_kernel" in r["Kernel_Name"]]
+    def phases(rows):
+        """Dispatches split at the marker launches (stream_read_kernel)."""
+        out, cur = [], []
+        for r in rows:
+            if "stream_read" in r["Kernel_Name"]:
+                out.append(cur)
+                cur = []
+            else:
+                cur.append(r)
+        out.append(cur)
+        return out
 
     def probe(rows, key):
         hits = [float(r["Counter_Value"]) for r in rows if key(r["Kernel_Name"].lower())]
         return max(hits) if hits else None
     f_probe = probe(fetch, lambda n: "reduce" in n)   # the 256 MiB sum reads 256 MiB
     w_probe = probe(write, lambda n: "fill" in n)     # the 256 MiB fill writes 256 MiB
-    fk, wk = ours(fetch), ours(write)
-    if not fk or len(fk) != len(wk) or not f_probe or not w_probe:
-        return None, "headline or calibration dispatches missing from the counter output"
+    fp, wp = phases(fetch), phases(write)
+    # phases: headline, int8 M=1, int8 M=64, (fp8 operands), fp8 GEMM, attention, MoE, calibration
+    if len(fp) != 8 or len(wp) != 8 or not f_probe or not w_probe:
+        return None, "phases or calibration dispatches missing from the counter output"
     f_scale = PROBE_BYTES / 1024 / f_probe
     w_scale = PROBE_BYTES / 1024 / w_probe
+
+    def ours(rows):
+        return [r for r in rows if "wo_" in r["Kernel_Name"] and "_kernel" in r["Kernel_Name"]]
+    fk, wk = ours(fp[0]), ours(wp[0])
+    if not fk or len(fk) != len(wk):
+        return None, "headline dispatches missing from the counter output"
     per_m = {}
     for i, (fr, wr) in enumerate(zip(fk, wk)):
         M = MS[i % len(MS)]
         per_m.setdefault(M, []).append((float(fr["Counter_Value"]) * f_scale + float(wr["Counter_Value"]) * w_scale) * 1024)
     means = {M: sum(v) / len(v) for M, v in per_m.items()}
+
+    def call_bytes(fr, wr):
+        tot = sum(float(r["Counter_Value"]) for r in fr) * f_scale + sum(float(r["Counter_Value"]) for r in wr) * w_scale
+        return round(tot * 1024 / TRAFFIC_CALLS)
+    # the kernels of each phase's calls (the phase also holds its setup: quantize, fills)
+    keep = [lambda n: "wo_" in n, lambda n: "wo_" in n, lambda n: "fp8_gemm" in n, lambda n: "paged_decode" in n,
+            lambda n: "moe" in n and "quantize" not in n]
+    sections = {}
+    for (name, key), sel, i in zip(TRAFFIC_PHASES, keep, (1, 2, 4, 5, 6)):
+        b = call_bytes([r for r in fp[i] if sel(r["Kernel_Name"])], [r for r in wp[i] if sel(r["Kernel_Name"])])
+        if key is None:
+            sections[name] = b
+        else:
+            sections.setdefault(name, {})[key] = b
     return {"bytes_per_launch": round(sum(means.values()) / len(means)),
             "per_M_bytes": {f"M={M}": round(v) for M, v in sorted(means.items())},
+            "sections": sections,
             "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
             "dispatches": len(fk)}, None
+
+
+def attach_traffic(breakdown, sections):
+    """Adds each configuration's measured HBM bytes per call (counter passes of this run)
+    beside its algorithmic bytes."""
+    def put(entry, traffic, algorithmic):
+        entry["traffic_bytes_per_call"] = traffic
+        entry["algorithmic_bytes_per_call"] = round(algorithmic)
+        entry["traffic_over_algorithmic"] = round(traffic / algorithmic, 3)
+    N8, K8 = 19456, 2560
+    for key, b in sections.get("int8_w8a16_gate_up_per_M", {}).items():
+        M = int(key.split("=")[1])
+        if key in breakdown.get("int8_w8a16_gate_up_per_M", {}):
+            put(breakdown["int8_w8a16_gate_up_per_M"][key], b, N8 * K8 + N8 * 4 + M * K8 * 2 + M * N8 * 2)
+    if "fp8_prefill_gemm" in sections and "fp8_prefill_gemm" in breakdown:
+        M, N, K = 2048, 6144, 2560
+        put(breakdown["fp8_prefill_gemm"], sections["fp8_prefill_gemm"], M * K + N * K + 4 * (M + N) + M * N * 2)
+    if "paged_decode_fp8_kv" in sections and "paged_decode_fp8_kv" in breakdown:
+        e = breakdown["paged_decode_fp8_kv"]
+        put(e, sections["paged_decode_fp8_kv"], e["MB_per_call"] * 1e6)
+        e["traffic_partition"] = e.get("default_partition")
+    if "moe_int4_layer" in sections and "moe_int4_layer" in breakdown:
+        e = breakdown["moe_int4_layer"]
+        put(e, sections["moe_int4_layer"], e["MB_per_call"] * 1e6)
 
 
 SECTIONS = {
@@ -777,6 +884,8 @@ def main():
             breakdown[name] = fn()
             torch.cuda.empty_cache()
             log(f"[bench]   {breakdown[name]}")
+    if traffic and args.only == "all":
+        attach_traffic(breakdown, traffic["sections"])
     cpu = None
     if not args.no_cpu:
         torch.set_num_threads(len(os.sched_getaffinity(0)))
