@@ -634,14 +634,15 @@ def cpu_moe(budget=6.0):
 
 # ---------------------------------------------------------------- HBM traffic (counters)
 # The phases of the counter child after the headline, in order: (breakdown entry, key)
-TRAFFIC_PHASES = [("int8_w8a16_gate_up_per_M", "M=1"), ("int8_w8a16_gate_up_per_M", "M=64"),
+TRAFFIC_PHASES = [("int8_w8a16_gate_up_per_M", "M=1"), ("int8_w8a16_gate_up_per_M", "M=8"),
+                  ("int8_w8a16_gate_up_per_M", "M=32"), ("int8_w8a16_gate_up_per_M", "M=64"),
                   ("fp8_prefill_gemm", None), ("paged_decode_fp8_kv", None), ("moe_int4_layer", None)]
 TRAFFIC_CALLS = 2  # calls per phase
 
 
 def traffic_child():
     """The run the counter passes watch: four headline launches per round, eagerly; then
-    TRAFFIC_CALLS calls of each TRAFFIC_PHASES configuration (INT8 gate_up at M = 1 and 64,
+    TRAFFIC_CALLS calls of each TRAFFIC_PHASES configuration (INT8 gate_up at every M,
     the FP8 GEMM, FP8-KV paged decode at the default partition, the INT4 MoE layer); then
     the two calibration kernels (a 256 MiB fill, and a sum over a 256 MiB buffer that a
     second fill has evicted from the MALL). A tiny miq_stream_read launch ends each phase,
@@ -665,7 +666,7 @@ def traffic_child():
     del cfg
     marker()
     c8 = int8_setup(dev)
-    for M in (1, 64):
+    for M in (1, 8, 32, 64):
         for i in range(TRAFFIC_CALLS):
             q, sc = c8["copies"][i % len(c8["copies"])]
             ops.w8a16_linear(c8["x"][M], q, sc)
@@ -752,8 +753,8 @@ def measure_traffic():
     f_probe = probe(fetch, lambda n: "reduce" in n)   # the 256 MiB sum reads 256 MiB
     w_probe = probe(write, lambda n: "fill" in n)     # the 256 MiB fill writes 256 MiB
     fp, wp = phases(fetch), phases(write)
-    # phases: headline, int8 M=1, int8 M=64, (fp8 operands), fp8 GEMM, attention, MoE, calibration
-    if len(fp) != 8 or len(wp) != 8 or not f_probe or not w_probe:
+    # phases: headline, int8 M=1, 8, 32, 64, (fp8 operands), fp8 GEMM, attention, MoE, calibration
+    if len(fp) != 10 or len(wp) != 10 or not f_probe or not w_probe:
         return None, "phases or calibration dispatches missing from the counter output"
     f_scale = PROBE_BYTES / 1024 / f_probe
     w_scale = PROBE_BYTES / 1024 / w_probe
@@ -773,10 +774,11 @@ def measure_traffic():
         tot = sum(float(r["Counter_Value"]) for r in fr) * f_scale + sum(float(r["Counter_Value"]) for r in wr) * w_scale
         return round(tot * 1024 / TRAFFIC_CALLS)
     # the kernels of each phase's calls (the phase also holds its setup: quantize, fills)
-    keep = [lambda n: "wo_" in n, lambda n: "wo_" in n, lambda n: "fp8_gemm" in n, lambda n: "paged_decode" in n,
+    wo = lambda n: "wo_" in n  # noqa: E731
+    keep = [wo, wo, wo, wo, lambda n: "fp8_gemm" in n, lambda n: "paged_decode" in n,
             lambda n: "moe" in n and "quantize" not in n]
     sections = {}
-    for (name, key), sel, i in zip(TRAFFIC_PHASES, keep, (1, 2, 4, 5, 6)):
+    for (name, key), sel, i in zip(TRAFFIC_PHASES, keep, (1, 2, 3, 4, 6, 7, 8)):
         b = call_bytes([r for r in fp[i] if sel(r["Kernel_Name"])], [r for r in wp[i] if sel(r["Kernel_Name"])])
         if key is None:
             sections[name] = b
