@@ -382,7 +382,12 @@ def test_w4a16_prefill(M, N, K, group, symmetric):
     want = O.int4_linear_fp32(x, **q)
     y = ops.w4a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV), None if symmetric else q["zero"].to(DEV))
     assert y.shape == (M, N)
-    within(y, want)
+    from test_gpu_wide import int4_ref_weights_product, wide_planned
+    if wide_planned(M, N):  # the wide kernel multiplies the reference's bf16 weights
+        within(y, int4_ref_weights_product(x, q))
+        assert rel(y, want) < 0.01
+    else:
+        within(y, want)
     assert workspace_is_zero()
 
 
