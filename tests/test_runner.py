@@ -198,3 +198,36 @@ def test_quantized_greedy_matches_oracle(name, method, kv):
               f"{oout[first]} vs GPU {out[first]}, logit gap {gap:.4f} (near-tie bar {near})", flush=True)
         assert gap <= near, f"prompt {i}: divergence at step {first} is not a near-tie ({gap:.3f})"
     print(f"  free-running: {same}/{total} tokens equal before the first divergence of each prompt", flush=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("method,tiles", [("int4_wo", "1"), ("int8_wo", "1"), ("int4_wo", "0")])
+def test_long_prompt_prefill_through_the_wide_kernel(method, tiles, miq_env):
+    """A 200-token prompt: its prefill linears have M = 200 rows, so with the wide kernel
+    forced (MIQ_WO_WIDE_MT=1; "0" runs the prefill kernel) the whole engine path runs through
+    it. Teacher-forced logits against the bf16 restatement, to the bounds above."""
+    from engine.core.kv_cache import KVCache
+    from engine.core.model_runner import ModelRunner, generate
+    from engine.quantization import get_method
+    from engine.quantization.loader import quantize_model
+    print(f"[case] long prompt {method} wide tiles={tiles}", flush=True)
+    miq_env("MIQ_WO_WIDE_MT", tiles)
+    dev = torch.device("cuda")
+    model = qwen3(torch.bfloat16)
+    m = get_method(method, device="cuda", compute_dtype=torch.bfloat16, group_size=128)
+    quantize_model(model, m, ["experts", "linear"], "cuda")
+    cfg = model.config
+    cache = KVCache("paged", cfg.num_hidden_layers, cfg.num_key_value_heads, 128, 64 * 16, torch.bfloat16, dev,
+                    block_size=16)
+    prompt = torch.randint(0, cfg.vocab_size, (200,), generator=torch.Generator().manual_seed(3)).tolist()
+    logits = []
+    out = generate(ModelRunner(model, cache), [prompt], [6], logits_out=logits)[0]
+    ref = oracle_model(model, torch.bfloat16)
+    want = teacher_forced_logits(cpu_runner(ref), prompt + out[:-1], len(prompt) - 1).float()
+    got = torch.stack(logits[0])
+    p99 = (got - want).abs().flatten().quantile(0.99).item()
+    top = want.max(dim=-1).values
+    gap = (top - want[torch.arange(len(out)), torch.tensor(out)]).max().item()
+    print(f"  logit |error| p99 {p99:.4f}, worst top-minus-chosen {gap:.4f}", flush=True)
+    assert p99 <= P99_TOL["default"]
+    assert gap <= NEAR_TIE["default"]
