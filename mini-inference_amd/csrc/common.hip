@@ -46,6 +46,8 @@ Tuning read_tuning() {
   t.wo_wide_mt = wmt ? atoi(wmt) : -1;
   const char* wmm = getenv("MIQ_WO_WIDE_MIN_M");
   t.wo_wide_min_m = wmm && atoi(wmm) > 0 ? atoi(wmm) : 65;
+  const char* wss = getenv("MIQ_WO_WIDE_S");
+  t.wo_wide_s = wss ? atoi(wss) : 0;
   t.fp8_old = flag("MIQ_FP8_OLD");
   const char* fw = getenv("MIQ_FP8_WAVES");
   t.fp8_four_waves = fw && atoi(fw) == 4;

@@ -206,6 +206,7 @@ struct Tuning {
   int wo_wide_mt;             // MIQ_WO_WIDE_MT: 32-row activation tiles per wavefront of the wide kernel
                               // (1..3 forced, 0 off, -1 planned)
   int wo_wide_min_m;          // MIQ_WO_WIDE_MIN_M: smallest M for the wide kernel (65)
+  int wo_wide_s;              // MIQ_WO_WIDE_S: K splits of the wide kernel (0: planned)
   bool fp8_old;               // MIQ_FP8_OLD: the previous FP8 GEMM kernel family
   bool fp8_four_waves;        // MIQ_FP8_WAVES=4
   bool fp8_quant_rows_wg;     // MIQ_FP8_QUANT_ROWS_WG: one workgroup per row in fp8_quantize_rows

@@ -198,7 +198,8 @@ int scratch_of_current_device(void** out) {
 extern "C" int miq_w4a16_gemm_noalloc(const void* x, int64_t ldx, const uint8_t* q, const void* scale,
                                       const void* zero, int sz_dtype, int64_t group, void* y, int64_t ldy,
                                       int64_t M, int64_t N, int64_t K, void* stream) {
-  // the wide kernel runs here only where its packed activations fit the scratch as well
+  // the wide kernel runs here only where its packed activations and partials fit the scratch
+  // as well (the prefill kernel otherwise)
   const size_t need = wo_gemm_workspace_bytes(M, N, K, 4, false);
   MIQ_REQUIRE(need <= kScratchBytes,
               "w4a16_gemm_noalloc: M=%lld N=%lld K=%lld needs %zu bytes of split-K scratch, above the %zu bytes "

@@ -36,6 +36,7 @@
 
 #include "miq_common.h"
 #include "wo_core.h"
+#include "wo_wide.h"
 
 namespace miq {
 namespace {
@@ -486,21 +487,11 @@ PrefillPlan plan_prefill(int kind, int64_t M, int64_t N, int64_t K, size_t count
 
 }  // namespace
 
-size_t wo_wide_pack_bytes(int64_t M, int64_t K, int mt);
-bool wo_wide_fits(int64_t M, int64_t K, int64_t N, int64_t ldw, int mt);
-int wo_wide_launch(int kind, int mt, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw,
-                   const void* scale, const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y,
-                   int64_t ldy, int64_t M, int N, int K, void* pack, size_t pack_bytes, hipStream_t st,
-                   const char* name);
-
-int wo_wide_plan(int64_t M, int64_t N);
-
-// Activation tiles per wavefront of the wide kernel for this call (0: the prefill kernel):
-// M from MIQ_WO_WIDE_MIN_M up and a plan that fills the GPU.
-static int wide_mt(int64_t M, int64_t N, int64_t K, int64_t ldw) {
-  if (tuning().wo_wide_mt == 0 || M < tuning().wo_wide_min_m) return 0;
-  const int mt = wo_wide_plan(M, N);
-  return mt > 0 && wo_wide_fits(M, K, N, ldw, mt) ? mt : 0;
+// Plan of the wide kernel for this call (mt = 0: the prefill kernel): M from MIQ_WO_WIDE_MIN_M
+// up, the wide kernel not switched off.
+static WidePlan wide_plan(int64_t M, int64_t N, int64_t K, int64_t ldw) {
+  if (tuning().wo_wide_mt == 0 || M < tuning().wo_wide_min_m) return WidePlan{};
+  return wo_wide_plan(M, N, K, ldw);
 }
 
 // Workspace bytes of a prefill call: the counter area, then the split-K partials or (with_wide)
@@ -509,9 +500,10 @@ size_t wo_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bi
                                   bool with_wide) {
   const PrefillPlan pl = plan_prefill(weight_bits == 4 ? KIND_INT4 : KIND_INT8, M, N, K, counter_bytes);
   const size_t split = pl.S > 1 ? counter_bytes + pl.partial_bytes : 0;
-  // the wide kernel's packed activations (ldw is not known here: its limit is checked at launch)
-  const int wmt = with_wide ? wide_mt(M, N, K, 0) : 0;
-  const size_t wide = wmt > 0 ? counter_bytes + wo_wide_pack_bytes(M, K, wmt) : 0;
+  // the wide kernel's packed activations and partials (ldw is not known here: its limit is
+  // checked at launch)
+  const WidePlan wp = with_wide ? wide_plan(M, N, K, 0) : WidePlan{};
+  const size_t wide = wp.mt > 0 ? counter_bytes + wp.bytes() : 0;
   return std::max(split, wide);
 }
 
@@ -522,10 +514,15 @@ int wo_prefill_launch(int kind, const uint16_t* x, int64_t ldx, const uint8_t* w
                       const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y, int64_t ldy, int64_t M,
                       int N, int K, void* workspace, size_t ws_bytes, size_t counter_bytes, hipStream_t st,
                       const char* name) {
-  const int wmt = wide_mt(M, N, K, ldw);
-  if (wmt > 0 && workspace != nullptr && ws_bytes >= counter_bytes + wo_wide_pack_bytes(M, K, wmt))
-    return wo_wide_launch(kind, wmt, x, ldx, w, ldw, scale, zero, sd, group_steps, ngroups, y, ldy, M, N, K,
-                          static_cast<char*>(workspace) + counter_bytes, ws_bytes - counter_bytes, st, name);
+  // the wide kernel where it is planned and its workspace fits (the no-allocation entry
+  // point's scratch may not hold it: then the prefill kernel)
+  if (workspace != nullptr && ws_bytes > counter_bytes) {
+    const WidePlan wp = wide_plan(M, N, K, ldw);
+    if (wp.mt > 0 && ws_bytes - counter_bytes >= wp.bytes())
+      return wo_wide_launch(kind, wp, x, ldx, w, ldw, scale, zero, sd, group_steps, ngroups, y, ldy, M, N, K,
+                            static_cast<char*>(workspace) + counter_bytes,
+                            ws_bytes - counter_bytes, st, name);
+  }
   MIQ_REQUIRE((int64_t)N * ldw < 0x7fff0000LL, "%s: weights of %lld bytes exceed 2 GiB", name, (long long)N * ldw);
   MIQ_REQUIRE(M * ldx < (1LL << 31), "%s: activations of %lld elements exceed 2^31", name, (long long)(M * ldx));
   const PrefillPlan pl = plan_prefill(kind, M, N, K, counter_bytes);

@@ -36,6 +36,7 @@
 
 #include "miq_common.h"
 #include "wo_core.h"
+#include "wo_wide.h"
 
 namespace miq {
 namespace {
@@ -64,6 +65,9 @@ struct WideParams {
   int xbytes, wbytes, sbytes;  // bytes of the packed activations, weights, scales
   bool vec_store;       // y 8-byte aligned with ldy % 4 == 0
   bool m_major;         // tiles ordered activation panel by activation panel
+  int S, split_steps;   // K splits and k-steps per split
+  float* part;          // S > 1: S fp32 partial outputs [M][N], split_stride floats apart
+  int64_t split_stride;
 };
 
 // f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order
@@ -178,10 +182,13 @@ wo_wide_kernel(WideParams p) {
   // panel by weight panel (all activation tiles of a panel in a row) or, with m_major,
   // activation panel by activation panel, so that the workgroups that read the same operand
   // block run on one XCD and share its L2; the launcher orders by the larger operand
-  const int T = p.tiles_m * p.tiles_n;
+  const int T = p.tiles_m * p.tiles_n, I = T * p.S;
   const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3;
-  const int tile = (int)((int64_t)T * xcd / 8) + local;
-  if (tile >= (int)((int64_t)T * (xcd + 1) / 8)) return;
+  const int item = (int)((int64_t)I * xcd / 8) + local;
+  if (item >= (int)((int64_t)I * (xcd + 1) / 8)) return;
+  // item = split * T + tile: the splits of a tile run in different rounds of the XCD's items
+  const int split = item / T, tile = item - split * T;
+  const int sb = split * p.split_steps, s_end = min(p.steps, sb + p.split_steps);  // this split's k-steps
   int tn, tm;
   if (p.m_major) {
     tm = tile / p.tiles_n;
@@ -213,7 +220,7 @@ wo_wide_kernel(WideParams p) {
   uint32_t sw[2], zw[2];
   auto load_w = [&](auto set_c, int s) {
     constexpr int set = decltype(set_c)::value;
-    const int off = wok && s < p.steps ? wbase + s * WSTEP : kOutW;
+    const int off = wok && s < s_end ? wbase + s * WSTEP : kOutW;
 #pragma unroll
     for (int l = 0; l < WL; ++l) {
       const auto v = __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 16 * l, 0);
@@ -261,7 +268,7 @@ wo_wide_kernel(WideParams p) {
     constexpr int set = decltype(set_c)::value;
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
-      const int off = s < p.steps ? xoff[i] + s * 8192 : kOutW;
+      const int off = s < s_end ? xoff[i] + s * 8192 : kOutW;
       const auto v = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 1024 * c, 0);
       a[set][i][c] = __builtin_bit_cast(bf16x8, v);
     }
@@ -320,25 +327,26 @@ wo_wide_kernel(WideParams p) {
     });
   };
 
-  // Two register sets and LDS buffers. Step s multiplies buffer s % 2 with activation set
-  // s % 2 while the weights of step s + 1 are dequantized into the other buffer; it requests
+  // Two register sets and LDS buffers, over the split's k-steps sb .. s_end - 1. Step s
+  // multiplies buffer (s - sb) % 2 with activation set (s - sb) % 2 while the weights of
+  // step s + 1 are dequantized into the other buffer; it requests
   // the weights of step s + 2 when it starts and the activations of sub-step c of step s + 1
   // at its sub-step c, so each request has a whole step to arrive and only one step of
   // activations occupies registers at a time. Steps past the end read zeros (activations)
   // and add nothing.
   constexpr auto C0 = std::integral_constant<int, 0>{};
-  load_w(C0, 0);
-  load_w(std::integral_constant<int, 1>{}, 1);
+  load_w(C0, sb);
+  load_w(std::integral_constant<int, 1>{}, sb + 1);
 #pragma unroll
-  for (int c = 0; c < 8; ++c) load_a(C0, 0, c);
+  for (int c = 0; c < 8; ++c) load_a(C0, sb, c);
   {
     float sc = 0.f, zz = 0.f;
-    group_sz(C0, 0, sc, zz);
+    group_sz(C0, sb, sc, zz);
 #pragma unroll
     for (int q = 0; q < 8; ++q) *reinterpret_cast<uint4*>(s_w[0] + w_slot(q)) = dequant_chunk(C0, q, sc, zz);
   }
   __syncthreads();
-  for (int s0 = 0; s0 < p.steps; s0 += 2) {
+  for (int s0 = sb; s0 < s_end; s0 += 2) {
     unroll_r<2>([&](auto ph_c) {
       constexpr int ph = decltype(ph_c)::value;
       const int s = s0 + ph;
@@ -349,6 +357,32 @@ wo_wide_kernel(WideParams p) {
   }
 
   // ---- epilogue: acc[i][t][4 g + v] = y[mw + 32 i + lane % 32][n0 + 32 t + 8 g + 4 (lane / 32) + v]
+  if (p.S > 1) {
+    // split K: this split's fp32 partial tile; wo_wide_reduce_kernel adds the splits
+    float* part = p.part + (int64_t)split * p.split_stride;
+#pragma unroll
+    for (int t = 0; t < kWNT; ++t)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + 32 * t + 8 * g + 4 * (lane >> 5);
+        if (n >= p.N) continue;
+#pragma unroll
+        for (int i = 0; i < MT; ++i) {
+          const int m = mw + 32 * i + (lane & 31);
+          if (m >= p.M) continue;
+          float* dst = part + (int64_t)m * p.N + n;
+          if ((p.N & 3) == 0) {
+            *reinterpret_cast<float4*>(dst) =
+                make_float4(acc[i][t][4 * g], acc[i][t][4 * g + 1], acc[i][t][4 * g + 2], acc[i][t][4 * g + 3]);
+          } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              if (n + v < p.N) dst[v] = acc[i][t][4 * g + v];
+          }
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < kWNT; ++t)
 #pragma unroll
@@ -413,37 +447,62 @@ __global__ void __launch_bounds__(256) wo_wide_clear_kernel(i32x4* __restrict__ 
     if (i + 256 * j < n16) p[i + 256 * j] = z;
 }
 
+// y = the sum of the S partial outputs of a split launch, in split order (the same sum
+// whichever workgroup finishes first), for int8 rounded to bf16 and scaled as the
+// unsplit epilogue does; the partials are overwritten with zeros (the workspace is zero
+// between calls). A thread takes 4 consecutive elements of the flattened [M][N] output
+// (16-byte loads: split_stride is a multiple of 4).
+template <bool I8, int SD>
+__global__ __launch_bounds__(256) void wo_wide_reduce_kernel(float* part, int64_t split_stride, int S, int M, int N,
+                                                             const void* scale, uint16_t* y, int64_t ldy) {
+  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  const int64_t MN = (int64_t)M * N;
+  if (e >= MN) return;
+  float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < S; s0 += 4) {
+    float4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      v[u] = s0 + u < S ? *reinterpret_cast<const float4*>(part + (s0 + u) * split_stride + e)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (s0 + u < S) *reinterpret_cast<float4*>(part + (s0 + u) * split_stride + e) = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      sum.x += v[u].x;
+      sum.y += v[u].y;
+      sum.z += v[u].z;
+      sum.w += v[u].w;
+    }
+  }
+  const float o[4] = {sum.x, sum.y, sum.z, sum.w};
+  int m = (int)(e / N), n = (int)(e - (int64_t)m * N);
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    if (e + v >= MN) break;
+    float val = o[v];
+    if constexpr (I8) val = bf16_to_f32(f32_to_bf16(val)) * bf16_to_f32(f32_to_bf16(sd_to_f32<SD>(load_sd_raw<SD>(scale, n))));
+    y[(int64_t)m * ldy + n] = f32_to_bf16(val);
+    if (++n == N) {
+      n = 0;
+      ++m;
+    }
+  }
+}
+
 template <int KIND, bool HZ, int SD, int MT>
 void launch_wide(const WideParams& p, hipStream_t st) {
-  const unsigned tiles = (unsigned)(p.tiles_m * p.tiles_n);
-  const unsigned grid = (tiles + 7) / 8 * 8 + 8;  // every XCD block fits its share
+  const unsigned items = (unsigned)(p.tiles_m * p.tiles_n * p.S);
+  const unsigned grid = (items + 7) / 8 * 8 + 8;  // every XCD block fits its share
   hipLaunchKernelGGL((wo_wide_kernel<KIND, HZ, SD, MT>), dim3(grid), dim3(256), 0, st, p);
 }
 
 }  // namespace
 
-// Activation tiles per wavefront (1..3) for a call, or 0 where the wide kernel would leave
-// most CUs idle (then the prefill kernel, whose smaller tiles and K splits fill the GPU,
-// is faster). A launch of T tiles takes ceil(T / 256) rounds (one workgroup per CU), each
-// as long as MT 32-row tiles; measured on MI355X the time per tile and k-step relative to
-// MT = 3 is 1.32 (MT = 1) and 1.13 (MT = 2) per 32-row tile. The MT of least modelled
-// time is taken (the larger on ties); below 128 tiles (half the CUs) none.
-int wo_wide_plan(int64_t M, int64_t N) {
-  const int forced = tuning().wo_wide_mt;
-  if (forced >= 1 && forced <= 3) return forced;
-  static const double kCost[4] = {0.0, 1.32, 1.13, 1.0};
-  const int64_t tiles_n = (N + kWN - 1) / kWN;
-  int best = 0;
-  double best_t = 0.0;
-  for (int mt = 1; mt <= 3; ++mt) {
-    const int64_t tiles = (M + 128 * mt - 1) / (128 * mt) * tiles_n;
-    const double t = (double)((tiles + 255) / 256) * mt * kCost[mt];
-    if (tiles >= 128 && (best == 0 || t <= best_t)) {
-      best = mt;
-      best_t = t;
-    }
-  }
-  return best;
+// Bytes of the fp32 partial outputs of a launch with S > 1 K splits (0 for S = 1).
+size_t wo_wide_part_bytes(int64_t M, int64_t N, int S) {
+  return S > 1 ? (size_t)S * (size_t)((M * N + 3) & ~3LL) * 4 : 0;
 }
 
 // Bytes of the packed activations of a call (32-row tiles of whole workgroups).
@@ -452,25 +511,79 @@ size_t wo_wide_pack_bytes(int64_t M, int64_t K, int mt) {
   return (size_t)(tiles_m * 4 * mt * 32) * (size_t)K * 2;
 }
 
-// Whether the wide kernel takes a call of this shape: the weights and the packed activations
-// must be addressable by buffer descriptors with an out-of-range offset to spare.
-bool wo_wide_fits(int64_t M, int64_t K, int64_t N, int64_t ldw, int mt) {
-  return mt >= 1 && mt <= 3 && wo_wide_pack_bytes(M, K, mt) < 0x7fff0000ULL && N * ldw < 0x7fff0000LL;
+// Plan of a call: activation tiles per wavefront (mt, 1..3; 0 = the wide kernel would leave
+// most CUs idle, so the prefill kernel, whose smaller tiles fill the GPU, runs instead) and
+// K splits (S). A launch of T tiles and S splits is T S workgroups in ceil(T S / 256) rounds
+// (one per CU), each as long as MT 32-row tiles over ceil(steps / S) k-steps (rounded up to
+// an even count: the loop takes steps in pairs). The modelled time is
+//   0.8 us * rounds * MT * c(MT) * k-steps  +  0.5 us per MB of fp32 partials (S > 1)
+// with c = 1.75, 1.13, 1.0 for MT = 1, 2, 3, fitted on MI355X to a sweep of every MT and
+// S = 1 .. 16 (N x K = 2560 x 9728, 4096 x 4096, 2560 x 2560, 6144 x 4096, 4096 x 12288;
+// M = 65 .. 4096), where the plan of least modelled time came within 1 % of the fastest on
+// average. The plan of least modelled time is taken (the larger MT, then the fewer splits,
+// on ties); plans below 128 workgroups (half the CUs) are not taken unless MT is forced
+// (MIQ_WO_WIDE_MT). Splits are planned only from 48 k-steps (K >= 6144) up: at shorter K
+// the pack, reduce and clear launches around a short split launch cost more than the
+// prefill kernel does (2560 x 2560 at M = 128 .. 768: 23-41 us split against 22-34 us),
+// while at K = 9728 and 12288 the split launch beats it by 10-35 % from M = 65 up. The plan
+// does not depend on the workspace a call brings: a call whose workspace cannot hold it
+// runs the prefill kernel instead.
+WidePlan wo_wide_plan(int64_t M, int64_t N, int64_t K, int64_t ldw) {
+  static const double kCost[4] = {0.0, 1.75, 1.13, 1.0};
+  constexpr int64_t kMinSplitSteps = 48;
+  const int forced_mt = tuning().wo_wide_mt, forced_s = tuning().wo_wide_s;
+  const int64_t tiles_n = (N + kWN - 1) / kWN, steps = K / kStepK;
+  const int max_s = forced_s >= 1 || steps >= kMinSplitSteps ? 16 : 1;
+  WidePlan best{};
+  double best_t = 0.0;
+  for (int mt = 1; mt <= 3; ++mt) {
+    if (forced_mt >= 1 && forced_mt <= 3 && mt != forced_mt) continue;
+    const size_t pack = wo_wide_pack_bytes(M, K, mt);
+    if (pack >= 0x7fff0000ULL || N * ldw >= 0x7fff0000LL) continue;
+    const int64_t tiles = (M + 128 * mt - 1) / (128 * mt) * tiles_n;
+    for (int S = 1; S <= max_s; ++S) {
+      const int64_t per = (steps + S - 1) / S;
+      if ((steps + per - 1) / per != S) continue;  // no empty splits
+      if (forced_s >= 1) {  // MIQ_WO_WIDE_S (at most 16 and steps), less any empty splits
+        const int64_t fs = std::min<int64_t>(std::min(forced_s, 16), steps);
+        if (per != (steps + fs - 1) / fs) continue;
+      }
+      const size_t part = wo_wide_part_bytes(M, N, S);
+      const int64_t items = tiles * S;
+      if (items < 128 && forced_mt < 1) continue;
+      const double t = 0.8 * (double)((items + 255) / 256) * mt * kCost[mt] * (double)((per + 1) & ~1LL) +
+                       (double)part * 0.5e-6;
+      if (best.mt == 0 || t < best_t - 1e-9 || (t <= best_t + 1e-9 && mt > best.mt)) {
+        best.mt = mt;
+        best.S = S;
+        best.split_steps = (int)per;
+        best.pack_bytes = pack;
+        best.part_bytes = part;
+        best_t = t;
+      }
+    }
+  }
+  return best;
 }
 
-// Launches the wide path: pack the activations into `pack` (workspace bytes that are zero
-// on entry), run the kernel, and clear `pack` again. Returns a MIQ_* status. `mt` =
-// activation tiles of 32 rows per wavefront (1, 2 or 3).
-int wo_wide_launch(int kind, int mt, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw,
+// Launches the wide path: pack the activations into the first pl.pack_bytes of `ws` (zero on
+// entry), run the kernel (with pl.S > 1 it writes fp32 partial outputs after the packed
+// activations, and the reduce kernel adds them into y and clears them), and clear the packed
+// activations again, so `ws` is zero afterwards. Returns a MIQ_* status.
+int wo_wide_launch(int kind, const WidePlan& pl, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw,
                    const void* scale, const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y,
-                   int64_t ldy, int64_t M, int N, int K, void* pack, size_t pack_bytes, hipStream_t st,
+                   int64_t ldy, int64_t M, int N, int K, void* ws, size_t ws_bytes, hipStream_t st,
                    const char* name) {
-  MIQ_REQUIRE(wo_wide_fits(M, K, N, ldw, mt), "%s: operands too large for the wide kernel", name);
-  const size_t need = wo_wide_pack_bytes(M, K, mt);
-  MIQ_REQUIRE(pack != nullptr && pack_bytes >= need && (reinterpret_cast<uintptr_t>(pack) & 15) == 0,
-              "%s: the wide kernel needs %zu bytes of aligned workspace, %zu given", name, need, pack_bytes);
+  const int mt = pl.mt;
+  MIQ_REQUIRE(mt >= 1 && mt <= 3 && pl.S >= 1 && pl.pack_bytes == wo_wide_pack_bytes(M, K, mt) &&
+                  pl.pack_bytes < 0x7fff0000ULL && (int64_t)N * ldw < 0x7fff0000LL,
+              "%s: operands too large for the wide kernel", name);
+  const size_t need = pl.pack_bytes + pl.part_bytes;
+  MIQ_REQUIRE(ws != nullptr && ws_bytes >= need && (reinterpret_cast<uintptr_t>(ws) & 15) == 0,
+              "%s: the wide kernel needs %zu bytes of aligned workspace, %zu given", name, need, ws_bytes);
+  MIQ_REQUIRE(pl.part_bytes == wo_wide_part_bytes(M, N, pl.S), "%s: inconsistent wide plan", name);
   WideParams p{};
-  p.x = static_cast<const uint16_t*>(pack);
+  p.x = static_cast<const uint16_t*>(ws);
   p.w = w;
   p.ldw = ldw;
   p.scale = scale;
@@ -484,18 +597,22 @@ int wo_wide_launch(int kind, int mt, const uint16_t* x, int64_t ldx, const uint8
   p.steps = K / kStepK;
   p.tiles_m = (int)((M + 128 * mt - 1) / (128 * mt));
   p.tiles_n = (N + kWN - 1) / kWN;
-  p.xbytes = (int)need;
+  p.xbytes = (int)pl.pack_bytes;
   p.wbytes = (int)((int64_t)N * ldw);
   const int esz = sd == MIQ_F32 ? 4 : 2;
   p.sbytes = kind == KIND_INT4 ? (int)(((int64_t)N * ngroups * esz + 3) & ~3LL) : 0;
   p.vec_store = (reinterpret_cast<uintptr_t>(y) & 7) == 0 && ldy % 4 == 0;
   // every XCD reads all of the operand its tiles do not share: keep the larger one shared
   // (each XCD then reads all of the smaller one)
-  p.m_major = (int64_t)need > (int64_t)N * ldw;
-  MIQ_REQUIRE((int64_t)p.tiles_m * p.tiles_n < (1LL << 30), "%s: too many tiles", name);
+  p.m_major = (int64_t)pl.pack_bytes > (int64_t)N * ldw;
+  p.S = pl.S;
+  p.split_steps = pl.S > 1 ? pl.split_steps : p.steps;
+  p.part = pl.S > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + pl.pack_bytes) : nullptr;
+  p.split_stride = (M * N + 3) & ~3LL;
+  MIQ_REQUIRE((int64_t)p.tiles_m * p.tiles_n * p.S < (1LL << 30), "%s: too many tiles", name);
   const int tiles32 = p.tiles_m * 4 * mt;
   hipLaunchKernelGGL(wo_wide_pack_kernel, dim3(p.steps, tiles32), dim3(256), 0, st, x, ldx, (int)M, p.steps,
-                     static_cast<uint16_t*>(pack));
+                     static_cast<uint16_t*>(ws));
 #define MIQ_WIDE_MT(K_, HZ_, SD_)                                   \
   do {                                                              \
     if (mt == 1) launch_wide<K_, HZ_, SD_, 1>(p, st);               \
@@ -513,9 +630,20 @@ int wo_wide_launch(int kind, int mt, const uint16_t* x, int64_t ldx, const uint8
   else MIQ_WIDE(KIND_INT4, false);
 #undef MIQ_WIDE
 #undef MIQ_WIDE_MT
-  const int64_t n16 = (int64_t)(need / 16);
+  if (pl.S > 1) {
+    const unsigned blocks = (unsigned)((M * N + 1023) / 1024);
+#define MIQ_WIDE_RED(I8_, SD_) \
+  hipLaunchKernelGGL((wo_wide_reduce_kernel<I8_, SD_>), dim3(blocks), dim3(256), 0, st, p.part, p.split_stride, p.S, \
+                     p.M, p.N, scale, y, ldy)
+    if (kind != KIND_INT8) MIQ_WIDE_RED(false, MIQ_F32);
+    else if (sd == MIQ_BF16) MIQ_WIDE_RED(true, MIQ_BF16);
+    else if (sd == MIQ_F16) MIQ_WIDE_RED(true, MIQ_F16);
+    else MIQ_WIDE_RED(true, MIQ_F32);
+#undef MIQ_WIDE_RED
+  }
+  const int64_t n16 = (int64_t)(pl.pack_bytes / 16);
   hipLaunchKernelGGL(wo_wide_clear_kernel, dim3((unsigned)((n16 + 1023) / 1024)), dim3(256), 0, st,
-                     static_cast<i32x4*>(pack), n16);
+                     static_cast<i32x4*>(ws), n16);
   return check_launch(name);
 }
 

@@ -383,7 +383,7 @@ def test_w4a16_prefill(M, N, K, group, symmetric):
     y = ops.w4a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV), None if symmetric else q["zero"].to(DEV))
     assert y.shape == (M, N)
     from test_gpu_wide import int4_ref_weights_product, wide_planned
-    if wide_planned(M, N):  # the wide kernel multiplies the reference's bf16 weights
+    if wide_planned(M, N, K):  # the wide kernel multiplies the reference's bf16 weights
         within(y, int4_ref_weights_product(x, q))
         assert rel(y, want) < 0.01
     else:

@@ -12,10 +12,11 @@ weights. (The exact fp32 product is not an elementwise bound for bf16 weights: a
 K = 9728 the weights' rounding alone moves outputs by up to about 0.04, the reference's
 own formula included.) INT8 codes are exact in bf16, so INT8 keeps the exact oracle.
 
-Every shape runs with each tile height forced (MIQ_WO_WIDE_MT = 1, 2, 3), with the planned
-choice, and with the wide kernel off (the prefill kernel, held to the exact oracle as in
-test_gpu_gemm), and the shared workspace must be all zeros afterwards (the packed
-activations are cleared again).
+Every shape runs with each tile height forced (MIQ_WO_WIDE_MT = 1, 2, 3), with K splits
+forced (MIQ_WO_WIDE_S: 1 to 16 splits, fp32 partial outputs added in split order by the
+reduce kernel), with the planned choice, and with the wide kernel off (the prefill kernel,
+held to the exact oracle as in test_gpu_gemm), and the shared workspace must be all zeros
+afterwards (the packed activations and the partials are cleared again).
 """
 import pytest
 import torch
@@ -29,13 +30,55 @@ pytestmark = pytest.mark.gpu
 # 128-row weight block (2576 = 20 * 128 + 16), one and three k-steps, groups of 1 to 4 steps
 WIDE_SHAPES = [(1300, 2560, 512, 128), (520, 2576, 1536, 256), (777, 1024, 128, 128), (300, 4096, 384, 128),
                (2048, 2560, 2560, 512), (1024, 2560, 9728, 128)]
-TILES = {"mt1": "1", "mt2": "2", "mt3": "3", "planned": None, "off": "0"}
+# MIQ_WO_WIDE_MT, MIQ_WO_WIDE_S: forced tile heights, forced K splits (fp32 partial outputs
+# added by the reduce kernel), the planned choice, the wide kernel off
+TILES = {"mt1": ("1", None), "mt2": ("2", None), "mt3": ("3", None), "mt1s3": ("1", "3"), "mt2s2": ("2", "2"),
+         "mt3s16": ("3", "16"), "planned": (None, None), "off": ("0", None)}
 
 
-def wide_planned(M, N):
-    """libmiq's planner (wo_wide_plan) takes the wide kernel when its smallest tiles
-    (128 x 128) number at least 128, half the CUs; the prefill kernel otherwise."""
-    return -(-M // 128) * -(-N // 128) >= 128
+def set_tiles(miq_env, tiles):
+    mt, s = TILES[tiles]
+    if mt is not None:
+        miq_env("MIQ_WO_WIDE_MT", mt)
+    if s is not None:
+        miq_env("MIQ_WO_WIDE_S", s)
+
+
+def wide_plan(M, N, K):
+    """libmiq's plan of the wide kernel (wo_wide_plan), restated: (MT, S, workspace bytes
+    past the counter area) or None where the prefill kernel runs (M below 65, or fewer than
+    128 workgroups in every plan). A launch of T tiles of 128 x 128 MT and S K splits runs
+    ceil(T S / 256) rounds of MT 32-row tiles over ceil(steps / S) k-steps (rounded up to
+    even), with relative cost 1.75 / 1.13 / 1.0 for MT = 1 / 2 / 3 and the partial outputs
+    priced at 0.5 us per MB; splits only from 48 k-steps up; the least modelled time wins,
+    the larger MT then the fewer splits on ties."""
+    if M < 65:
+        return None
+    cost = {1: 1.75, 2: 1.13, 3: 1.0}
+    tiles_n, steps = -(-N // 128), K // 128
+    max_s = 16 if steps >= 48 else 1
+    best, best_t = None, 0.0
+    for mt in (1, 2, 3):
+        tm = -(-M // (128 * mt))
+        pack = tm * 4 * mt * 32 * K * 2
+        if pack >= 0x7fff0000:
+            continue
+        for S in range(1, max_s + 1):
+            per = -(-steps // S)
+            if -(-steps // per) != S:
+                continue
+            part = S * ((M * N + 3) & ~3) * 4 if S > 1 else 0
+            items = tm * tiles_n * S
+            if items < 128:
+                continue
+            t = 0.8 * float(-(-items // 256)) * mt * cost[mt] * float((per + 1) & ~1) + float(part) * 0.5e-6
+            if best is None or t < best_t - 1e-9 or (t <= best_t + 1e-9 and mt > best[0]):
+                best, best_t = (mt, S, pack + part), t
+    return best
+
+
+def wide_planned(M, N, K):
+    return wide_plan(M, N, K) is not None
 
 
 def int4_ref_weights_product(x, q):
@@ -77,13 +120,12 @@ def int8_case(M, N, K, sdt):
 def test_w4a16_wide(M, N, K, group, symmetric, sdt, tiles, miq_env):
     from kernels import quant_ops as ops
     case(f"w4a16 wide M={M} N={N} K={K} g={group} sym={symmetric} {sdt} tiles={tiles}")
-    if TILES[tiles] is not None:
-        miq_env("MIQ_WO_WIDE_MT", TILES[tiles])
+    set_tiles(miq_env, tiles)
     x, q, ref_w, exact = int4_case(M, N, K, group, symmetric, sdt)
     y = ops.w4a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV),
                          None if symmetric else q["zero"].to(DEV))
     assert y.shape == (M, N)
-    if tiles == "off" or (tiles == "planned" and not wide_planned(M, N)):
+    if tiles == "off" or (tiles == "planned" and not wide_planned(M, N, K)):
         within(y, exact)  # the prefill kernel: exact weights, as in test_gpu_gemm
     else:
         within(y, ref_w)
@@ -97,8 +139,7 @@ def test_w4a16_wide(M, N, K, group, symmetric, sdt, tiles, miq_env):
 def test_w8a16_wide(M, N, K, sdt, tiles, miq_env):
     from kernels import quant_ops as ops
     case(f"w8a16 wide M={M} N={N} K={K} {sdt} tiles={tiles}")
-    if TILES[tiles] is not None:
-        miq_env("MIQ_WO_WIDE_MT", TILES[tiles])
+    set_tiles(miq_env, tiles)
     x, q, want, ref = int8_case(M, N, K, sdt)
     y = ops.w8a16_linear(x.to(DEV), q["qweight"].to(DEV), q["scale"].to(DEV))
     within(y, want)

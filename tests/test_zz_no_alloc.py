@@ -45,11 +45,10 @@ def with_workspace(x, q):
 
 def test_noalloc_matches_workspace_entry_point():
     # (M, N, K, group, symmetric): the panel kernel with its largest scratch at config 2, the
-    # prefill kernel with a K split (200 rows: 80 tiles), a smaller panel launch, two
-    # tile-kernel launches of the two-half plan (exchange words in the scratch), then the
-    # first shape again
-    # the wide kernel (1024 rows: its packed activations, 2 MiB, go in the scratch and are
-    # cleared again) comes between the prefill and panel launches
+    # wide kernel with 10 K splits (200 rows: packed activations and fp32 partials, 24.3 MiB,
+    # in the scratch and cleared again), the wide kernel unsplit (1024 rows, 2 MiB), a
+    # smaller panel launch, two tile-kernel launches of the two-half plan (exchange words in
+    # the scratch), then the first shape again
     shapes = [(64, 2560, 9728, 128, True), (200, 2560, 9728, 128, False), (1024, 2560, 1024, 128, False),
               (40, 1280, 4096, 256, False), (16, 2560, 9728, 128, True), (8, 512, 1024, 128, False),
               (64, 2560, 9728, 128, True)]
@@ -64,15 +63,15 @@ def test_noalloc_matches_workspace_entry_point():
         # and within the north-star tolerance of the fp32 oracle: the exactly dequantized
         # weights, or for the wide kernel the reference's own bf16 weights (test_gpu_wide)
         qc = {k: v.cpu() for k, v in q.items()}
-        ref = (int4_ref_weights_product(x.cpu(), qc) if M > 64 and wide_planned(M, N)
+        ref = (int4_ref_weights_product(x.cpu(), qc) if M > 64 and wide_planned(M, N, K)
                else O.int4_linear_fp32(x.cpu(), **qc))
         err = (y.float().cpu() - ref).abs()
         assert (err <= 1e-2 + 2e-2 * ref.abs()).all()
 
 
 def test_noalloc_large_prefill_takes_the_prefill_kernel():
-    """2048 x 9728 activations: the wide kernel's packed copy (40 MiB) would not fit the
-    32 MiB scratch, so the entry point runs the prefill kernel (split-K partials within the
+    """2048 x 9728 activations: the wide kernel's plan (a 40 MiB packed copy and two K
+    splits' fp32 partials, 83 MiB in all) would not fit the 32 MiB scratch, so the entry point runs the prefill kernel (split-K partials within the
     scratch) where the workspace entry point runs the wide kernel: both within the
     north-star tolerance of the fp32 oracle, and the scratch left clean for the next call."""
     M, N, K, group = 2048, 2560, 9728, 128
