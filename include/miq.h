@@ -120,10 +120,10 @@ int miq_fp8_dequantize(const uint8_t* q, const float* scale, int64_t rows, int64
  * its 128 x 128..384 tiles fill the GPU (long prefill chunks), a GEMM that dequantizes
  * each weight block once per workgroup for the bf16 MFMA.
  * Workspace for the split-K reduction of the two weight-only GEMMs and for the last
- * kernel's packed activations. Its first 16384 bytes hold arrival counters that must be
- * zero before the first call (zero the whole buffer once when allocating it); every call
- * leaves the whole workspace at zero again (counters, fp32 partials and packed
- * activations alike). A workspace below this size for a long prefill call makes it take
+ * kernel's packed activations and K-split partials. Its first 16384 bytes hold arrival
+ * counters that must be zero before the first call (zero the whole buffer once when
+ * allocating it); every call leaves the whole workspace at zero again (counters, fp32
+ * partials and packed activations alike). A workspace below this size for a long prefill call makes it take
  * the prefill kernel. Calls that share one workspace must be ordered (same stream). */
 size_t miq_wo_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, int weight_bits);
 
@@ -153,7 +153,7 @@ int miq_w4a16_gemm(const void* x, int64_t ldx, const uint8_t* q, const void* sca
  * hipMalloc). No counterpart in the reference. The split-K scratch is a static device array
  * of 32 MiB that each GPU holds until the process ends; shapes whose split-K scratch
  * exceeds it are rejected (MIQ_ERR_INVALID); long prefill calls whose packed activations
- * would not fit take the prefill kernel. Every call on a GPU shares that GPU's array: calls that
+ * and K-split partials would not fit take the prefill kernel. Every call on a GPU shares that GPU's array: calls that
  * overlap on one GPU (two streams, two threads) race and give wrong results; calls ordered
  * on one stream are safe. Allocates nothing; the first call on a device looks up the
  * array's address there. Same arguments and results as miq_w4a16_gemm. */
