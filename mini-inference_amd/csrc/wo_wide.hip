@@ -452,10 +452,21 @@ __global__ void __launch_bounds__(256) wo_wide_clear_kernel(i32x4* __restrict__ 
 // unsplit epilogue does; the partials are overwritten with zeros (the workspace is zero
 // between calls). A thread takes 4 consecutive elements of the flattened [M][N] output
 // (16-byte loads: split_stride is a multiple of 4).
+// The packed activations are cleared by the same launch: its first clear_blocks workgroups
+// run wo_wide_clear_kernel's work, the others the reduction.
 template <bool I8, int SD>
 __global__ __launch_bounds__(256) void wo_wide_reduce_kernel(float* part, int64_t split_stride, int S, int M, int N,
-                                                             const void* scale, uint16_t* y, int64_t ldy) {
-  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+                                                             const void* scale, uint16_t* y, int64_t ldy,
+                                                             i32x4* pack, int64_t n16, int clear_blocks) {
+  if ((int)blockIdx.x < clear_blocks) {
+    const i32x4 z = {0, 0, 0, 0};
+    const int64_t i = (int64_t)blockIdx.x * 1024 + threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (i + 256 * j < n16) pack[i + 256 * j] = z;
+    return;
+  }
+  const int64_t e = ((int64_t)(blockIdx.x - clear_blocks) * 256 + threadIdx.x) * 4;
   const int64_t MN = (int64_t)M * N;
   if (e >= MN) return;
   float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -569,7 +580,8 @@ WidePlan wo_wide_plan(int64_t M, int64_t N, int64_t K, int64_t ldw) {
 // Launches the wide path: pack the activations into the first pl.pack_bytes of `ws` (zero on
 // entry), run the kernel (with pl.S > 1 it writes fp32 partial outputs after the packed
 // activations, and the reduce kernel adds them into y and clears them), and clear the packed
-// activations again, so `ws` is zero afterwards. Returns a MIQ_* status.
+// activations again (in the reduce kernel's launch when there is one), so `ws` is zero
+// afterwards. Returns a MIQ_* status.
 int wo_wide_launch(int kind, const WidePlan& pl, const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t ldw,
                    const void* scale, const void* zero, int sd, int group_steps, int64_t ngroups, uint16_t* y,
                    int64_t ldy, int64_t M, int N, int K, void* ws, size_t ws_bytes, hipStream_t st,
@@ -630,20 +642,22 @@ int wo_wide_launch(int kind, const WidePlan& pl, const uint16_t* x, int64_t ldx,
   else MIQ_WIDE(KIND_INT4, false);
 #undef MIQ_WIDE
 #undef MIQ_WIDE_MT
+  // clear the packed activations again (with K splits, in the reduce kernel's launch)
+  const int64_t n16 = (int64_t)(pl.pack_bytes / 16);
+  const unsigned clear_blocks = (unsigned)((n16 + 1023) / 1024);
   if (pl.S > 1) {
-    const unsigned blocks = (unsigned)((M * N + 1023) / 1024);
-#define MIQ_WIDE_RED(I8_, SD_) \
-  hipLaunchKernelGGL((wo_wide_reduce_kernel<I8_, SD_>), dim3(blocks), dim3(256), 0, st, p.part, p.split_stride, p.S, \
-                     p.M, p.N, scale, y, ldy)
+    const unsigned blocks = clear_blocks + (unsigned)((M * N + 1023) / 1024);
+#define MIQ_WIDE_RED(I8_, SD_)                                                                                  \
+  hipLaunchKernelGGL((wo_wide_reduce_kernel<I8_, SD_>), dim3(blocks), dim3(256), 0, st, p.part, p.split_stride, \
+                     p.S, p.M, p.N, scale, y, ldy, static_cast<i32x4*>(ws), n16, (int)clear_blocks)
     if (kind != KIND_INT8) MIQ_WIDE_RED(false, MIQ_F32);
     else if (sd == MIQ_BF16) MIQ_WIDE_RED(true, MIQ_BF16);
     else if (sd == MIQ_F16) MIQ_WIDE_RED(true, MIQ_F16);
     else MIQ_WIDE_RED(true, MIQ_F32);
 #undef MIQ_WIDE_RED
+  } else {
+    hipLaunchKernelGGL(wo_wide_clear_kernel, dim3(clear_blocks), dim3(256), 0, st, static_cast<i32x4*>(ws), n16);
   }
-  const int64_t n16 = (int64_t)(pl.pack_bytes / 16);
-  hipLaunchKernelGGL(wo_wide_clear_kernel, dim3((unsigned)((n16 + 1023) / 1024)), dim3(256), 0, st,
-                     static_cast<i32x4*>(ws), n16);
   return check_launch(name);
 }
 
