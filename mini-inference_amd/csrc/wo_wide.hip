@@ -186,7 +186,8 @@ wo_wide_kernel(WideParams p) {
   const int xcd = blockIdx.x & 7, local = blockIdx.x >> 3;
   const int item = (int)((int64_t)I * xcd / 8) + local;
   if (item >= (int)((int64_t)I * (xcd + 1) / 8)) return;
-  // item = split * T + tile: the splits of a tile run in different rounds of the XCD's items
+  // item = split * T + tile: XCDs take contiguous blocks of items, so an XCD's workgroups
+  // share one split's K range of the weights and activations
   const int split = item / T, tile = item - split * T;
   const int sb = split * p.split_steps, s_end = min(p.steps, sb + p.split_steps);  // this split's k-steps
   int tn, tm;
