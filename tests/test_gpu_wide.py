@@ -136,11 +136,15 @@ def test_wide_strided_rows_and_output():
     torch.testing.assert_close(buf[:, :N], ops.w4a16_linear(xd, qd, sd, zd), rtol=0, atol=0)
 
 
-def test_wide_graph_replays_match_eager():
-    """Pack, multiply and clear under HIP graph capture: every replay (with eager work and a
+@pytest.mark.parametrize("K", [1024, 9728])
+def test_wide_graph_replays_match_eager(K):
+    """Pack, multiply and clear under HIP graph capture (K = 9728: the planned K splits, with
+    the reduce kernel adding and clearing the partials): every replay (with eager work and a
     synchronization between replays) matches the eager result bit for bit."""
     from kernels import quant_ops as ops
-    M, N, K = 1024, 2560, 1024
+    M, N = 1024, 2560
+    case(f"wide graph replays M={M} N={N} K={K} plan={wide_plan(M, N, K)}")
+    assert wide_plan(M, N, K)[1] == (1 if K == 1024 else 3)
     w = make_w(N, K, 96)
     q = O.int4_quantize(w, 128)
     qd, sd, zd = (q[k].to(DEV) for k in ("qweight", "scale", "zero"))
